@@ -1,0 +1,262 @@
+"""Benchmark of the MI355X block-FP8 W8A8 GEMM (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|mlp]
+
+Workload (one "step"): the BASELINE configs[1] decode sweep -- one block-FP8
+GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
+E4M3 weights with fp32 128x128 block scales, bf16 activations quantized per
+1x128 group inside the op, bf16 output.  Inputs are synthetic (seeded
+N(0,0.02) weights with 5% x8 blocks, N(0,1) activations with 1% x20 outlier
+channels) and resident in HBM before timing starts.  Weight copies totalling
+>= 512 MB are rotated so the 256 MB Infinity Cache cannot serve them.
+
+value = algorithmic bytes of the sweep / time per sweep (GB/s), with bytes per
+GEMM B = N*K + 4*ceil(N/128)*ceil(K/128) + 2*M*K + 2*M*N.  Side measurements
+in the same JSON line: the prefill config (M=4096, N=K=7168; TFLOP/s against
+the dense FP8 MFMA peak), the MLP-pair decode config, the per-M sweep, the
+roofline of the dominant kernel (decode GEMM, HIP events on its stream) and
+the CPU oracle baseline timed on this host.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gaudi-kernels_amd", "python"))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "block-FP8 GEMM GB/s & TFLOP/s (% roofline) at M=1..16 and M=4096"
+PEAK_HBM_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5033.0   # dense, 256 CU x 8192 FLOP/clk x 2.4 GHz
+MALL_ROTATE_BYTES = 512 << 20
+
+
+def gemm_bytes(m, n, k, bias=False):
+    nb, g = (n + 127) // 128, (k + 127) // 128
+    return n * k + 4 * nb * g + 2 * m * k + 2 * m * n + (4 * n if bias else 0)
+
+
+def gemm_flops(m, n, k):
+    return 2 * m * n * k
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Rotation:
+    """Distinct device copies of one weight/scale pair totalling >= MALL_ROTATE_BYTES."""
+
+    def __init__(self, w, s, min_bytes=MALL_ROTATE_BYTES):
+        copies = max(1, -(-min_bytes // (w.numel() + 4 * s.numel())))
+        wd, sd = w.cuda(), s.cuda()
+        self.items = [(wd, sd)] + [(wd.clone(), sd.clone()) for _ in range(copies - 1)]
+        self.i = 0
+
+    def next(self):
+        item = self.items[self.i]
+        self.i = (self.i + 1) % len(self.items)
+        return item
+
+
+def capture(fn, iters):
+    """HIP graph of `iters` back-to-back fn() calls (kernel launches only; no host work at replay)."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn()  # first call outside capture (library / allocator warm-up)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, iters_in_graph, replays=3):
+    """Average ms per captured call, HIP events on the replay stream (torch's current stream)."""
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / (replays * iters_in_graph)
+
+
+def time_loop(fn, iters, warmup):
+    """Average ms per fn() call: `warmup` eager calls, then a graph of `iters` calls replayed."""
+    for _ in range(warmup):
+        fn()
+    return time_graph(capture(fn, iters), iters)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--only", choices=["decode", "prefill", "mlp"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU runs its own shard, "
+              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from gaudi_kernels import ops
+    from oracle import synth
+
+    ops.require_device()
+    dev_name = torch.cuda.get_device_name(0)
+    log(f"[bench] device {dev_name}")
+    result = {}
+
+    # ---- config 2: decode sweep (the timed step) ----------------------------------------------
+    n, k = 6144, 4096
+    ms_list = (1, 2, 4, 8, 16)
+    w, s = synth.weight(n, k, seed=2000)
+    rot = Rotation(w, s)
+    xs = {m: synth.activations(m, k, seed=2001 + m).cuda() for m in ms_list}
+    outs = {m: torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for m in ms_list}
+    wss = {m: torch.empty(ops.plan(m, n, k)[2] + 256, dtype=torch.uint8, device="cuda") for m in ms_list}
+    sweep_bytes = sum(gemm_bytes(m, n, k) for m in ms_list)
+    sweep_flops = sum(gemm_flops(m, n, k) for m in ms_list)
+
+    def step():
+        for m in ms_list:
+            wd, sd = rot.next()
+            ops.block_fp8_gemm(xs[m], wd, sd, out=outs[m], workspace=wss[m])
+
+    # The K timed steps (and the W warm-up steps) are captured as HIP graphs so
+    # that the GPU runs them back to back without per-launch host work.
+    log(f"[bench] decode sweep: {len(rot.items)} weight copies, warmup {args.warmup}, steps {args.steps}")
+    g_warm = capture(step, max(1, args.warmup))
+    g_timed = capture(step, args.steps)
+    g_warm.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    g_timed.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    del g_warm, g_timed
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"[bench] decode sweep {ms_per_step * 1e3:.1f} us/step, {value:.0f} GB/s (wall {wall:.3f}s)")
+
+    # per-M: whole op (quant + GEMM) and the GEMM kernel alone (pre-quantized activations)
+    per_m = {}
+    kernel_us_m16 = None
+    for m in ms_list:
+        op_ms = time_loop(lambda: ops.block_fp8_gemm(xs[m], *rot.next(), out=outs[m], workspace=wss[m]), 100, 10)
+        _, m_pad, _ = ops.plan(m, n, k)
+        q, sa = ops.act_quant(xs[m], m_pad=m_pad)
+        kern_ms = time_loop(lambda: ops.block_fp8_gemm_q(q, sa, m, *rot.next(), out=outs[m]), 100, 10)
+        b = gemm_bytes(m, n, k)
+        per_m[str(m)] = {"op_us": round(op_ms * 1e3, 2), "gemm_kernel_us": round(kern_ms * 1e3, 2),
+                         "op_GBps": round(b / (op_ms * 1e-3) / 1e9, 1),
+                         "gemm_kernel_GBps": round(b / (kern_ms * 1e-3) / 1e9, 1),
+                         "gemm_kernel_hbm_frac": round(b / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        if m == 16:
+            kernel_us_m16 = kern_ms * 1e3
+        log(f"[bench]   M={m}: op {op_ms * 1e3:.2f} us, gemm kernel {kern_ms * 1e3:.2f} us "
+            f"({per_m[str(m)]['gemm_kernel_GBps']} GB/s)")
+    del rot
+    torch.cuda.empty_cache()
+
+    b16 = gemm_bytes(16, n, k)
+    achieved = b16 / (kernel_us_m16 * 1e-6) / 1e9
+    result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                          "kernel": "gk::gemm_decode_kernel (M=16, N=6144, K=4096)",
+                          "bytes_per_launch": b16, "avg_launch_us": round(kernel_us_m16, 3)}
+    result["decode_sweep"] = per_m
+
+    # ---- config 3: MLP pair decode at M=16 ------------------------------------------------------
+    if args.only in (None, "mlp"):
+        m = 16
+        pair = []
+        for (nn, kk, seed) in ((28672, 4096, 3000), (4096, 14336, 3100)):
+            w3, s3 = synth.weight(nn, kk, seed=seed)
+            r3 = Rotation(w3, s3)
+            x3 = synth.activations(m, kk, seed=seed + 1).cuda()
+            o3 = torch.empty((m, nn), dtype=torch.bfloat16, device="cuda")
+            ws3 = torch.empty(ops.plan(m, nn, kk)[2] + 256, dtype=torch.uint8, device="cuda")
+            ms3 = time_loop(lambda: ops.block_fp8_gemm(x3, *r3.next(), out=o3, workspace=ws3), 30, 5)
+            pair.append((nn, kk, ms3))
+            del r3
+            torch.cuda.empty_cache()
+        tb = sum(gemm_bytes(m, nn, kk) for nn, kk, _ in pair)
+        tt = sum(t for _, _, t in pair)
+        result["mlp_pair_m16"] = {"us": round(tt * 1e3, 2), "GBps": round(tb / (tt * 1e-3) / 1e9, 1),
+                                  "hbm_frac": round(tb / (tt * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                  "gate_up_us": round(pair[0][2] * 1e3, 2), "down_us": round(pair[1][2] * 1e3, 2)}
+        log(f"[bench] mlp pair: {result['mlp_pair_m16']}")
+
+    # ---- config 4: prefill ------------------------------------------------------------------------
+    if args.only in (None, "prefill"):
+        m, nn, kk = 4096, 7168, 7168
+        w4, s4 = synth.weight(nn, kk, seed=4000)
+        x4 = synth.activations(m, kk, seed=4001).cuda()
+        w4d, s4d = w4.cuda(), s4.cuda()
+        o4 = torch.empty((m, nn), dtype=torch.bfloat16, device="cuda")
+        ws4 = torch.empty(ops.plan(m, nn, kk)[2] + 256, dtype=torch.uint8, device="cuda")
+        ms4 = time_loop(lambda: ops.block_fp8_gemm(x4, w4d, s4d, out=o4, workspace=ws4), 20, 3)
+        _, m_pad, _ = ops.plan(m, nn, kk)
+        q4, sa4 = ops.act_quant(x4, m_pad=m_pad)
+        ms4k = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, w4d, s4d, out=o4), 20, 3)
+        f = gemm_flops(m, nn, kk)
+        result["prefill_m4096"] = {"op_us": round(ms4 * 1e3, 1), "gemm_kernel_us": round(ms4k * 1e3, 1),
+                                   "op_TFLOPs": round(f / (ms4 * 1e-3) / 1e12, 1),
+                                   "gemm_kernel_TFLOPs": round(f / (ms4k * 1e-3) / 1e12, 1),
+                                   "gemm_kernel_mfma_frac": round(f / (ms4k * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+        log(f"[bench] prefill: {result['prefill_m4096']}")
+
+    # ---- CPU baseline: the oracle on this host ----------------------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        from oracle import block_fp8
+        cores = os.cpu_count() or 1
+        torch.set_num_threads(cores)
+        m = 16
+        xc = synth.activations(m, k, seed=2001 + m)
+        block_fp8.reference(xc[:1], w, s)  # warm-up
+        times = []
+        t_budget = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_budget < 10 and len(times) < 10):
+            t1 = time.perf_counter()
+            block_fp8.reference(xc, w, s, row_chunk=16)
+            times.append(time.perf_counter() - t1)
+        tmed = sorted(times)[len(times) // 2]
+        cpu = {"value": round(gemm_bytes(m, n, k) / tmed / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": f"oracle/block_fp8.reference, config2 M=16 N=6144 K=4096, median of {len(times)} runs "
+                         f"({tmed * 1e3:.0f} ms each), torch threads={cores}"}
+        log(f"[bench] cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3", "data": "synthetic",
+        "config": {"workload": "config2 QKV decode sweep: block-FP8 GEMM at M=1,2,4,8,16, N=6144, K=4096, "
+                               "128x128 fp32 weight scales, 1x128 activation groups, bf16 out",
+                   "sweep_bytes": sweep_bytes, "sweep_flops": sweep_flops, "device": dev_name},
+        **result,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,336 @@
+// C ABI of libgk_fp8.so (declared in include/gk_fp8.h).
+//
+// Host-side validation, planning and dispatch.  The op table and status
+// codes mirror the Synapse provider of the reference
+// (csrc/host/generic_dense_glue.cpp:897-1013, generic_fp8_glue.hpp): a static
+// name table with a count query, int status codes, no exceptions, and the
+// same rejection classes (scale grid mismatch -> INCOMPATIBLE_INPUT_SIZE,
+// bad parameters -> UNSUPPORTED_LAYER_CONFIGURATION).  Unlike the glue, which
+// runs at graph-compile time, these entry points launch the kernels directly
+// on the caller's stream.
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <mutex>
+
+#include "../../include/gk_fp8.h"
+#include "gk_fp8_internal.h"
+
+namespace {
+
+constexpr const char* kOps[] = {
+    "gk_fp8_codec_ocp_to_half_v1",  // fp8_codec.py:14-53
+    "gk_fp8_codec_half_to_ocp_v1",  // inverse codec (build-defined)
+    "gk_fp8_act_quant_bf16_v1",     // activation_native.c:9-30 with block_fp8_oracle.py:25-28 numerics
+    "gk_fp8_block_gemm_bf16_v1",    // quant -> MME -> reduce_bias.c / prefill chain, fused
+    "gk_fp8_block_gemm_q_bf16_v1",  // GEMM on pre-quantized activations
+    "gk_fp8_check_inputs_v1",       // block_fp8_oracle.py:22-24
+};
+constexpr uint32_t kNumOps = sizeof(kOps) / sizeof(kOps[0]);
+
+constexpr uint32_t kKnownFlags =
+    GK_FLAG_NATIVE_HALF | GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL | GK_FLAG_FORCE_GENERIC;
+constexpr size_t kStatusBytes = 256;
+constexpr int64_t kMaxDim = (int64_t{1} << 31) - 1;
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
+
+gk_status from_hip(hipError_t e) { return e == hipSuccess ? GK_SUCCESS : GK_DEVICE_ERROR; }
+
+// Per-device gfx950 gate, evaluated once per device.
+constexpr int kMaxDevices = 64;
+std::once_flag g_dev_once[kMaxDevices];
+bool g_dev_ok[kMaxDevices];
+
+bool device_ok(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return false;
+  std::call_once(g_dev_once[dev], [dev] {
+    hipDeviceProp_t prop;
+    g_dev_ok[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+                    std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  });
+  return g_dev_ok[dev];
+}
+
+gk_status current_device_ok() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return GK_DEVICE_ERROR;
+  return device_ok(dev) ? GK_SUCCESS : GK_UNSUPPORTED_DEVICE;
+}
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  if (static_cast<int>(threadIdx.x) < n) p[threadIdx.x] = 0u;
+}
+
+// Status block in the caller's workspace: word 0 = flags, words 2..3 = 64-bit count.
+struct Status {
+  uint32_t flags;
+  uint32_t pad;
+  unsigned long long count;
+};
+
+gk_status read_status(void* ws, Status* st, hipStream_t stream) {
+  if (hipMemcpyAsync(st, ws, sizeof(Status), hipMemcpyDeviceToHost, stream) != hipSuccess) return GK_DEVICE_ERROR;
+  return from_hip(hipStreamSynchronize(stream));
+}
+
+__global__ __launch_bounds__(256) void check_inputs_kernel(const uint16_t* __restrict__ x, int64_t m, int64_t k,
+                                                           int64_t ldx, const uint8_t* __restrict__ w,
+                                                           int64_t nw, const float* __restrict__ s, int64_t ns,
+                                                           uint32_t* __restrict__ flags) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint32_t bad = 0;
+  for (int64_t i = tid; i < m * k; i += stride) {
+    const int64_t r = i / k, c = i - r * k;
+    bad |= (x[r * ldx + c] & 0x7f80u) == 0x7f80u;
+  }
+  for (int64_t i = tid; i < nw; i += stride) bad |= (w[i] & 0x7fu) == 0x7fu;
+  for (int64_t i = tid; i < ns; i += stride) {
+    const float v = s[i];
+    bad |= !(v >= 0.0f) || (gk::f32_bits(v) & 0x7f800000u) == 0x7f800000u;
+  }
+  if (bad) atomicOr(flags, 1u);
+}
+
+struct Plan {
+  int variant;
+  int64_t m_pad;
+  size_t q_bytes, sa_bytes;
+};
+
+gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, Plan* p) {
+  if (m < 1 || n < 1 || k < 1 || m > kMaxDim || n > kMaxDim || k > kMaxDim) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (flags & ~kKnownFlags) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  const uint32_t force = flags & (GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL | GK_FLAG_FORCE_GENERIC);
+  if (force & (force - 1)) return GK_UNSUPPORTED_LAYER_CONFIGURATION;  // more than one forced variant
+  const bool tiled_ok = (k % 128 == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
+  int variant;
+  if (force == GK_FLAG_FORCE_GENERIC || (!force && !tiled_ok)) {
+    variant = GK_VARIANT_GENERIC;
+  } else if (!tiled_ok) {
+    return GK_UNSUPPORTED_LAYER_CONFIGURATION;  // decode/prefill need K % 128 == 0 and 16-byte aligned weights
+  } else if (force == GK_FLAG_FORCE_PREFILL) {
+    variant = GK_VARIANT_PREFILL;
+  } else if (force == GK_FLAG_FORCE_DECODE) {
+    if (m > gk::kDecodeMaxRows) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+    variant = GK_VARIANT_DECODE;
+  } else {
+    variant = m <= gk::kDecodeMaxRows ? GK_VARIANT_DECODE : GK_VARIANT_PREFILL;
+  }
+  const int64_t g = (k + 127) / 128;
+  p->variant = variant;
+  p->m_pad = variant == GK_VARIANT_DECODE ? gk::kDecodeMaxRows
+             : variant == GK_VARIANT_PREFILL ? round_up(m, gk::kPrefillRowTile)
+                                             : m;
+  p->q_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 128);
+  p->sa_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 4);
+  return GK_SUCCESS;
+}
+
+gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* scales, int64_t scale_rows,
+                            int64_t scale_cols, const void* y, int64_t ldy) {
+  if (!w || !scales || !y) return GK_INVALID_ARGUMENT;
+  if (scale_rows != (n + 127) / 128 || scale_cols != (k + 127) / 128) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldy < n) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(scales) & 3) || (reinterpret_cast<uintptr_t>(y) & 1))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  return GK_SUCCESS;
+}
+
+gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, int64_t k, const void* w, int64_t n,
+                   const float* scales, const float* bias, void* y, int64_t ldy, uint32_t flags,
+                   hipStream_t stream) {
+  gk::GemmArgs a;
+  a.qa = q;
+  a.sa = sa;
+  a.w = static_cast<const uint8_t*>(w);
+  a.sw = scales;
+  a.bias = bias;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = static_cast<int>(m);
+  a.N = static_cast<int>(n);
+  a.K = static_cast<int>(k);
+  a.G = static_cast<int>((k + 127) / 128);
+  a.Mpad = static_cast<int>(p.m_pad);
+  a.half_w = (flags & GK_FLAG_NATIVE_HALF) != 0;
+  hipError_t e;
+  switch (p.variant) {
+    case GK_VARIANT_DECODE: e = gk::launch_gemm_decode(a, stream); break;
+    case GK_VARIANT_PREFILL: e = gk::launch_gemm_prefill(a, stream); break;
+    default: e = gk::launch_gemm_generic(a, stream); break;
+  }
+  return from_hip(e);
+}
+
+gk_status codec_common(bool forward, const void* src, void* dst, int64_t n, const float* scales, float* scales_out,
+                       int64_t n_scales, int64_t* rounded, void* ws, size_t wsb, void* stream) {
+  if (!src || !dst || !scales || !scales_out || !ws) return GK_INVALID_ARGUMENT;
+  if (n < 1) return GK_INCOMPATIBLE_INPUT_SIZE;         // "expected a nonempty ... weight"
+  if (n_scales < 1) return GK_INVALID_SCALE;            // "expected nonempty ... scales"
+  if (wsb < kStatusBytes) return GK_INSUFFICIENT_BUFFER;
+  if (reinterpret_cast<uintptr_t>(ws) & 7) return GK_INCOMPATIBLE_DATA_TYPE;
+  if (reinterpret_cast<uintptr_t>(scales) & 3 || reinterpret_cast<uintptr_t>(scales_out) & 3)
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* words = static_cast<uint32_t*>(ws);
+  zero_words_kernel<<<1, 64, 0, s>>>(words, 4);
+  if (hipGetLastError() != hipSuccess) return GK_DEVICE_ERROR;
+  const hipError_t e = gk::launch_codec(forward, static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), n,
+                                        scales, scales_out, n_scales, words,
+                                        reinterpret_cast<unsigned long long*>(words + 2), s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  Status stat;
+  st = read_status(ws, &stat, s);
+  if (st != GK_SUCCESS) return st;
+  if (forward) {
+    if (stat.flags & 2u) return GK_INVALID_SCALE;
+    if (stat.flags & 4u) return GK_SCALE_OVERFLOW;
+    if (stat.flags & 1u) return GK_NONFINITE_CODE;
+    if (rounded) *rounded = static_cast<int64_t>(stat.count);
+  } else {
+    if (stat.flags & 2u) return GK_INVALID_SCALE;
+    if (stat.flags & 8u) return GK_NONFINITE_CODE;
+    if (stat.flags & 16u) return GK_INEXACT_SCALE;
+  }
+  return GK_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t gk_lib_version(void) { return 1; }
+
+gk_status gk_list_ops(uint32_t* count, const char** names) {
+  if (!count) return GK_INVALID_ARGUMENT;
+  const uint32_t capacity = *count;
+  *count = kNumOps;
+  if (!names || capacity == 0) return GK_SUCCESS;
+  const uint32_t emit = capacity < kNumOps ? capacity : kNumOps;
+  for (uint32_t i = 0; i < emit; ++i) names[i] = kOps[i];
+  return capacity < kNumOps ? GK_INSUFFICIENT_BUFFER : GK_SUCCESS;
+}
+
+gk_status gk_device_supported(int device) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return GK_DEVICE_ERROR;
+  if (device < 0 || device >= count) return GK_UNSUPPORTED_DEVICE;
+  return device_ok(device) ? GK_SUCCESS : GK_UNSUPPORTED_DEVICE;
+}
+
+gk_status gk_fp8_codec_workspace_bytes(size_t* bytes) {
+  if (!bytes) return GK_INVALID_ARGUMENT;
+  *bytes = kStatusBytes;
+  return GK_SUCCESS;
+}
+
+gk_status gk_fp8_codec_ocp_to_half(const void* src, void* dst, int64_t n, const float* scales, float* scales_out,
+                                   int64_t n_scales, int64_t* rounded, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return codec_common(true, src, dst, n, scales, scales_out, n_scales, rounded, workspace, workspace_bytes, stream);
+}
+
+gk_status gk_fp8_codec_half_to_ocp(const void* src, void* dst, int64_t n, const float* scales, float* scales_out,
+                                   int64_t n_scales, void* workspace, size_t workspace_bytes, void* stream) {
+  return codec_common(false, src, dst, n, scales, scales_out, n_scales, nullptr, workspace, workspace_bytes,
+                      stream);
+}
+
+gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, void* q, float* sa, int64_t m_pad,
+                                uint32_t flags, void* stream) {
+  if (!x || !q || !sa) return GK_INVALID_ARGUMENT;
+  if (m < 1 || k < 1 || m > kMaxDim || k > kMaxDim || ldx < k) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (m_pad < m || m_pad > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if ((reinterpret_cast<uintptr_t>(x) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
+      (reinterpret_cast<uintptr_t>(sa) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_act_quant(static_cast<const uint16_t*>(x), ldx, static_cast<int>(m),
+                                       static_cast<int>(k), static_cast<int>(m_pad), static_cast<uint8_t*>(q), sa,
+                                       (flags & GK_FLAG_NATIVE_HALF) != 0, static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, int* variant,
+                                 int64_t* m_pad, size_t* workspace_bytes) {
+  Plan p;
+  const gk_status st = make_plan(m, n, k, flags, w, &p);
+  if (st != GK_SUCCESS) return st;
+  if (variant) *variant = p.variant;
+  if (m_pad) *m_pad = p.m_pad;
+  if (workspace_bytes) *workspace_bytes = p.q_bytes + p.sa_bytes;
+  return GK_SUCCESS;
+}
+
+gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
+                                 const float* scales, int64_t scale_rows, int64_t scale_cols, const float* bias,
+                                 void* y, int64_t ldy, uint32_t flags, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (!x || !workspace) return GK_INVALID_ARGUMENT;
+  Plan p;
+  gk_status st = make_plan(m, n, k, flags, w, &p);
+  if (st != GK_SUCCESS) return st;
+  if (ldx < k) return GK_INCOMPATIBLE_INPUT_SIZE;
+  st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, y, ldy);
+  if (st != GK_SUCCESS) return st;
+  if (workspace_bytes < p.q_bytes + p.sa_bytes) return GK_INSUFFICIENT_BUFFER;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) || (reinterpret_cast<uintptr_t>(x) & 1))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* q = static_cast<uint8_t*>(workspace);
+  float* sa = reinterpret_cast<float*>(q + p.q_bytes);
+  hipError_t e = gk::launch_act_quant(static_cast<const uint16_t*>(x), ldx, static_cast<int>(m), static_cast<int>(k),
+                                      static_cast<int>(p.m_pad), q, sa, (flags & GK_FLAG_NATIVE_HALF) != 0, s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  return run_gemm(p, q, sa, m, k, w, n, scales, bias, y, ldy, flags, s);
+}
+
+gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, int64_t m_pad, int64_t k,
+                                   const void* w, int64_t n, const float* scales, int64_t scale_rows,
+                                   int64_t scale_cols, const float* bias, void* y, int64_t ldy, uint32_t flags,
+                                   void* stream) {
+  if (!q || !sa) return GK_INVALID_ARGUMENT;
+  Plan p;
+  gk_status st = make_plan(m, n, k, flags, w, &p);
+  if (st != GK_SUCCESS) return st;
+  if (m_pad != p.m_pad) return GK_INCOMPATIBLE_INPUT_SIZE;
+  st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, y, ldy);
+  if (st != GK_SUCCESS) return st;
+  if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(sa) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return run_gemm(p, static_cast<const uint8_t*>(q), sa, m, k, w, n, scales, bias, y, ldy, flags,
+                  static_cast<hipStream_t>(stream));
+}
+
+gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
+                              const float* scales, int64_t n_scales, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (!x || !w || !scales || !workspace) return GK_INVALID_ARGUMENT;
+  if (m < 1 || k < 1 || n < 1 || ldx < k || n_scales < 1) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (workspace_bytes < kStatusBytes) return GK_INSUFFICIENT_BUFFER;
+  gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* words = static_cast<uint32_t*>(workspace);
+  zero_words_kernel<<<1, 64, 0, s>>>(words, 4);
+  check_inputs_kernel<<<1024, 256, 0, s>>>(static_cast<const uint16_t*>(x), m, k, ldx,
+                                           static_cast<const uint8_t*>(w), n * k, scales, n_scales, words);
+  if (hipGetLastError() != hipSuccess) return GK_DEVICE_ERROR;
+  Status stat;
+  st = read_status(workspace, &stat, s);
+  if (st != GK_SUCCESS) return st;
+  return stat.flags ? GK_NONFINITE_INPUT : GK_SUCCESS;
+}
+
+}  // extern "C"

@@ -1,0 +1,246 @@
+// gfx950 kernels for the load-time E4M3 codec and the 1x128 activation quantizer.
+//
+// Codec (forward, OCP E4M3FN -> Gaudi2 half range) restates
+// python/gaudi_kernels/fp8_codec.py:14-53 of the reference: a per-byte table
+// (evaluated here as 4-byte SWAR arithmetic, gk_fp8_math.h), scales x2, a count
+// of rounded codes, rejection of the OCP NaN code and of scales that are
+// negative, nonfinite or overflow when doubled.  The inverse (half -> OCP) is
+// build-defined: value x2 (exact), scales / 2.
+//
+// Both are HBM-streaming byte kernels: one 16-byte load and one 16-byte store
+// per lane per step, grid-stride, with the per-wave rounded count reduced in
+// registers and one 64-bit atomic per wave.
+//
+// The activation quantizer restates block_fp8_oracle.py:25-28 (and :31-34 for
+// native_half): per row and 128-column group, sa = fp32(max(amax, 1e-10)) *
+// fp32(1/448), q = e4m3_rne(clamp(fp32(x / sa), +-448)) with an IEEE divide.
+// Sixteen lanes own one group (8 bf16 each, one 16-byte load per lane).
+
+#include "gk_fp8_internal.h"
+
+namespace gk {
+
+// Status flags written by the codec kernels (bit OR into flags[0]).
+enum : uint32_t {
+  kFlagNanCode = 1u,       // OCP NaN code in the forward input
+  kFlagBadScale = 2u,      // negative or nonfinite scale
+  kFlagScaleOverflow = 4u, // doubling overflows fp32
+  kFlagInvalidHalf = 8u,   // half-range magnitude >= 0x77 in the inverse input
+  kFlagInexactHalve = 16u, // halving a scale is inexact (fp32 subnormal result)
+};
+
+__device__ inline uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ inline uint32_t wave_or_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v |= __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <bool FORWARD>
+__global__ __launch_bounds__(256) void codec_bytes_kernel(const uint8_t* __restrict__ src,
+                                                          uint8_t* __restrict__ dst, int64_t n,
+                                                          uint32_t* __restrict__ flags,
+                                                          unsigned long long* __restrict__ rounded) {
+  const int64_t nvec = n >> 4;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint32_t bad = 0, count = 0;
+  const uint4* s4 = reinterpret_cast<const uint4*>(src);
+  uint4* d4 = reinterpret_cast<uint4*>(dst);
+  for (int64_t i = tid; i < nvec; i += stride) {
+    const uint4 v = s4[i];
+    uint4 o;
+    if (FORWARD) {
+      bad |= ocp_nan4(v.x) | ocp_nan4(v.y) | ocp_nan4(v.z) | ocp_nan4(v.w);
+      count += codec_rounded4(v.x) + codec_rounded4(v.y) + codec_rounded4(v.z) + codec_rounded4(v.w);
+      o.x = codec_half4(v.x); o.y = codec_half4(v.y); o.z = codec_half4(v.z); o.w = codec_half4(v.w);
+    } else {
+      bad |= half_invalid4(v.x) | half_invalid4(v.y) | half_invalid4(v.z) | half_invalid4(v.w);
+      o.x = codec_double4(v.x); o.y = codec_double4(v.y); o.z = codec_double4(v.z); o.w = codec_double4(v.w);
+    }
+    d4[i] = o;
+  }
+  // Tail bytes (n % 16): one byte per thread of the first block.
+  if (blockIdx.x == 0) {
+    for (int64_t j = (nvec << 4) + threadIdx.x; j < n; j += blockDim.x) {
+      const uint32_t v = src[j];
+      if (FORWARD) {
+        bad |= ocp_nan4(v) & 0x80u;
+        count += codec_rounded4(v) & 1u;
+        dst[j] = static_cast<uint8_t>(codec_half4(v));
+      } else {
+        bad |= half_invalid4(v) & 0x80u;
+        dst[j] = static_cast<uint8_t>(codec_double4(v));
+      }
+    }
+  }
+  count = wave_sum_u32(count);
+  bad = wave_or_u32(bad);
+  if ((threadIdx.x & 63) == 0) {
+    if (count) atomicAdd(rounded, static_cast<unsigned long long>(count));
+    if (bad) atomicOr(flags, FORWARD ? kFlagNanCode : kFlagInvalidHalf);
+  }
+}
+
+// Byte-granular variant for buffers that are not 16-byte aligned.
+template <bool FORWARD>
+__global__ __launch_bounds__(256) void codec_unaligned_kernel(const uint8_t* __restrict__ src,
+                                                              uint8_t* __restrict__ dst, int64_t n,
+                                                              uint32_t* __restrict__ flags,
+                                                              unsigned long long* __restrict__ rounded) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  uint32_t bad = 0, count = 0;
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < n; j += stride) {
+    const uint32_t v = src[j];
+    if (FORWARD) {
+      bad |= ocp_nan4(v) & 0x80u;
+      count += codec_rounded4(v) & 1u;
+      dst[j] = static_cast<uint8_t>(codec_half4(v));
+    } else {
+      bad |= half_invalid4(v) & 0x80u;
+      dst[j] = static_cast<uint8_t>(codec_double4(v));
+    }
+  }
+  count = wave_sum_u32(count);
+  bad = wave_or_u32(bad);
+  if ((threadIdx.x & 63) == 0) {
+    if (count) atomicAdd(rounded, static_cast<unsigned long long>(count));
+    if (bad) atomicOr(flags, FORWARD ? kFlagNanCode : kFlagInvalidHalf);
+  }
+}
+
+// Scales: forward doubles, inverse halves; both validate (finite, >= 0).
+template <bool FORWARD>
+__global__ __launch_bounds__(256) void codec_scales_kernel(const float* __restrict__ s, float* __restrict__ out,
+                                                           int64_t n, uint32_t* __restrict__ flags) {
+  uint32_t f = 0;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float v = s[i];
+    const uint32_t b = f32_bits(v);
+    if (!(v >= 0.0f) || (b & 0x7f800000u) == 0x7f800000u) f |= kFlagBadScale;  // NaN, inf, negative
+    if (FORWARD) {
+      const float d = v * 2.0f;
+      if ((f32_bits(d) & 0x7f800000u) == 0x7f800000u) f |= kFlagScaleOverflow;
+      out[i] = d;
+    } else {
+      if ((b & 0x7f800000u) <= 0x00800000u && (b & 1u)) f |= kFlagInexactHalve;
+      out[i] = v * 0.5f;
+    }
+  }
+  f = wave_or_u32(f);
+  if ((threadIdx.x & 63) == 0 && f) atomicOr(flags, f);
+}
+
+// ---- activation quantizer ----------------------------------------------------
+// x: bf16 [M, K] with row stride ldx (elements).  q: [Mpad, G*128] codes (rows
+// >= M and columns >= K are written as zero), sa: [Mpad, G] fp32 (zero for rows
+// >= M).  One group = 16 lanes x 8 elements.
+template <bool HALF>
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                        int K, int G, int Mpad, uint8_t* __restrict__ q,
+                                                        float* __restrict__ sa, int vec_ok) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const int64_t total = static_cast<int64_t>(Mpad) * G;
+  const bool active = gid < total;
+  const int64_t row = active ? gid / G : 0;
+  const int g = active ? static_cast<int>(gid - row * G) : 0;
+  const int col = g * 128 + sub * 8;
+  float v[8];
+  if (active && row < M && col + 8 <= K && vec_ok) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(x + row * ldx + col);
+    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bits_f32(w4[i] << 16);
+      v[2 * i + 1] = bits_f32(w4[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = (active && row < M && col + i < K) ? bf16_value(x[row * ldx + col + i]) : 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  // block_fp8_oracle.py:27 -- clamp_min(1e-10) then fp32 multiply by fp32(1/448).
+  const float s = fmaxf(amax, 1e-10f) * (1.0f / 448.0f);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float t = v[i] / s;                       // IEEE fp32 division (correctly rounded)
+    t = fminf(fmaxf(t, -448.0f), 448.0f);
+    const uint32_t c = e4m3_rne(t);
+    if (i < 4) lo |= c << (8 * i); else hi |= c << (8 * (i - 4));
+  }
+  if (HALF) {  // block_fp8_oracle.py:32,34: e4m3fn(qa * 0.5), sa * 2
+    lo = codec_half4(lo);
+    hi = codec_half4(hi);
+  }
+  if (active) {
+    const bool live = row < M;
+    *reinterpret_cast<uint2*>(q + row * static_cast<int64_t>(G) * 128 + col) = live ? make_uint2(lo, hi) : make_uint2(0u, 0u);
+    if (sub == 0) sa[row * G + g] = live ? (HALF ? s * 2.0f : s) : 0.0f;
+  }
+}
+
+// ---- launchers -----------------------------------------------------------------
+static int codec_grid(int64_t nvec) {
+  int64_t blocks = (nvec + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 8192) blocks = 8192;  // grid-stride beyond 32 blocks per CU
+  return static_cast<int>(blocks);
+}
+
+hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t n, const float* scales,
+                        float* scales_out, int64_t n_scales, uint32_t* flags, unsigned long long* rounded,
+                        hipStream_t stream) {
+  const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+  if (vec) {
+    const int blocks = codec_grid(n >> 4);
+    if (forward)
+      codec_bytes_kernel<true><<<blocks, 256, 0, stream>>>(src, dst, n, flags, rounded);
+    else
+      codec_bytes_kernel<false><<<blocks, 256, 0, stream>>>(src, dst, n, flags, rounded);
+  } else {
+    const int blocks = codec_grid(n);
+    if (forward)
+      codec_unaligned_kernel<true><<<blocks, 256, 0, stream>>>(src, dst, n, flags, rounded);
+    else
+      codec_unaligned_kernel<false><<<blocks, 256, 0, stream>>>(src, dst, n, flags, rounded);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (n_scales > 0) {
+    const int sblocks = codec_grid(n_scales / 16 + 1);
+    if (forward)
+      codec_scales_kernel<true><<<sblocks, 256, 0, stream>>>(scales, scales_out, n_scales, flags);
+    else
+      codec_scales_kernel<false><<<sblocks, 256, 0, stream>>>(scales, scales_out, n_scales, flags);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
+                            bool half, hipStream_t stream) {
+  const int G = (K + 127) / 128;
+  const int64_t groups = static_cast<int64_t>(Mpad) * G;
+  const int blocks = static_cast<int>((groups + 15) / 16);  // 16 groups per 256-thread block
+  const int vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (ldx % 8 == 0);
+  if (half)
+    act_quant_kernel<true><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok);
+  else
+    act_quant_kernel<false><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok);
+  return hipGetLastError();
+}
+
+}  // namespace gk

@@ -1,0 +1,198 @@
+"""Device-side block-FP8 operations on PyTorch-ROCm tensors (thin wrappers over libgk_fp8.so).
+
+These are the fast-path entry points: no host synchronisation (except the
+codec and the finite-input check, which read a status word back), caller's
+current HIP stream, workspaces from the PyTorch caching allocator.  The
+reference-compatible functions (``block_fp8_oracle.reference`` and
+``fp8_codec.reencode_e4m3fn_half``) are built on these.
+
+Layouts (row-major): x bf16 [M, K] (unit column stride), weight E4M3 codes
+[N, K] contiguous (torch.float8_e4m3fn or uint8), scales fp32
+[ceil(N/128), ceil(K/128)] contiguous, bias fp32 [N], output bf16 [M, N].
+"""
+
+import ctypes
+
+import torch
+
+from gaudi_kernels import _native as nat
+
+_DEVICE_OK = {}
+
+
+def require_device(device=None):
+    """Return the torch.device to run on; raise if it is not a gfx950 GPU with the library loaded."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("gaudi_kernels: no GPU visible (the block-FP8 path has no CPU fallback)")
+    if device is None or device.type != "cuda":
+        device = torch.device("cuda", torch.cuda.current_device())
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _DEVICE_OK:
+        lib = nat.load()
+        _DEVICE_OK[idx] = lib.gk_device_supported(idx) == nat.GK_SUCCESS
+    if not _DEVICE_OK[idx]:
+        raise RuntimeError(f"gaudi_kernels: device cuda:{idx} is not a gfx950 GPU")
+    return torch.device("cuda", idx)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _u8(t):
+    return t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t
+
+
+def plan(m, n, k, flags=0, weight=None):
+    """(variant, m_pad, workspace_bytes) that gk_fp8_block_gemm_bf16 uses for these sizes."""
+    lib = nat.load()
+    variant = ctypes.c_int(0)
+    m_pad = ctypes.c_int64(0)
+    ws = ctypes.c_size_t(0)
+    wp = _ptr(weight) if weight is not None else ctypes.c_void_p(256)
+    nat.check("gk_fp8_block_gemm_plan",
+              lib.gk_fp8_block_gemm_plan(m, n, k, flags, wp, ctypes.byref(variant), ctypes.byref(m_pad),
+                                         ctypes.byref(ws)))
+    return variant.value, m_pad.value, ws.value
+
+
+def _flags(native_half, variant):
+    flags = nat.GK_FLAG_NATIVE_HALF if native_half else 0
+    if variant is not None:
+        flags |= {"decode": nat.GK_FLAG_FORCE_DECODE, "prefill": nat.GK_FLAG_FORCE_PREFILL,
+                  "generic": nat.GK_FLAG_FORCE_GENERIC}[variant]
+    return flags
+
+
+def act_quant(x, *, native_half=False, m_pad=None):
+    """1x128 activation quantization on the GPU -> (codes uint8 [m_pad, G*128], sa fp32 [m_pad, G])."""
+    device = require_device(x.device)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("expected a 2-D bf16 activation with unit column stride")
+    m, k = x.shape
+    g = (k + 127) // 128
+    m_pad = m if m_pad is None else m_pad
+    q = torch.empty((m_pad, g * 128), dtype=torch.uint8, device=device)
+    sa = torch.empty((m_pad, g), dtype=torch.float32, device=device)
+    lib = nat.load()
+    nat.check("gk_fp8_act_quant_bf16",
+              lib.gk_fp8_act_quant_bf16(_ptr(x), m, k, x.stride(0), _ptr(q), _ptr(sa), m_pad,
+                                        nat.GK_FLAG_NATIVE_HALF if native_half else 0, _stream(device)))
+    return q, sa
+
+
+def _check_gemm_operands(weight, scales, bias, device):
+    if weight.dtype not in (torch.float8_e4m3fn, torch.uint8) or weight.ndim != 2 or not weight.is_contiguous():
+        raise ValueError("expected a contiguous 2-D E4M3 weight [N, K]")
+    if scales.dtype != torch.float32 or scales.ndim != 2 or not scales.is_contiguous():
+        raise ValueError("expected contiguous fp32 block scales [ceil(N/128), ceil(K/128)]")
+    if weight.device != device or scales.device != device or (bias is not None and bias.device != device):
+        raise ValueError("all operands must be on the same GPU")
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != weight.shape[0]):
+        raise ValueError("expected a contiguous fp32 bias with N elements")
+
+
+def block_fp8_gemm(x, weight, scales, bias=None, *, native_half=False, variant=None, out=None, workspace=None):
+    """y = block-FP8 W8A8 linear of bf16 x [M, K] with E4M3 weight [N, K] -> bf16 [M, N] (asynchronous).
+
+    variant: None (dispatch by M), "decode", "prefill" or "generic".
+    workspace: optional uint8 device tensor of at least plan(...)[2] + 256 bytes (reused across calls;
+    calls that share one workspace must be ordered on one stream).
+    """
+    device = require_device(x.device)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("expected a 2-D bf16 activation with unit column stride")
+    _check_gemm_operands(weight, scales, bias, device)
+    m, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError("activation and weight K differ")
+    flags = _flags(native_half, variant)
+    w8 = _u8(weight)
+    _, _, ws_bytes = plan(m, n, k, flags, w8)
+    ws = workspace
+    if ws is None or ws.numel() < ws_bytes + 256:
+        if ws is not None:
+            raise ValueError(f"workspace too small: need {ws_bytes + 256} bytes")
+        ws = torch.empty(max(ws_bytes, 256) + 256, dtype=torch.uint8, device=device)
+    ws_ptr = (ws.data_ptr() + 255) // 256 * 256
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    elif out.dtype != torch.bfloat16 or out.shape != (m, n) or out.stride(1) != 1 or out.device != device:
+        raise ValueError("out must be bf16 [M, N] with unit column stride on the same GPU")
+    lib = nat.load()
+    nat.check("gk_fp8_block_gemm_bf16",
+              lib.gk_fp8_block_gemm_bf16(_ptr(x), m, k, x.stride(0), _ptr(w8), n, _ptr(scales), scales.shape[0],
+                                         scales.shape[1], _ptr(bias), _ptr(out), out.stride(0), flags,
+                                         ctypes.c_void_p(ws_ptr), ws.numel() - (ws_ptr - ws.data_ptr()),
+                                         _stream(device)))
+    return out
+
+
+def block_fp8_gemm_q(q, sa, m, weight, scales, bias=None, *, native_half=False, variant=None, out=None):
+    """GEMM on activations already quantized by act_quant(m_pad=plan(...)[1])."""
+    device = require_device(q.device)
+    _check_gemm_operands(weight, scales, bias, device)
+    n, k = weight.shape
+    flags = _flags(native_half, variant)
+    w8 = _u8(weight)
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    lib = nat.load()
+    nat.check("gk_fp8_block_gemm_q_bf16",
+              lib.gk_fp8_block_gemm_q_bf16(_ptr(q), _ptr(sa), m, q.shape[0], k, _ptr(w8), n, _ptr(scales),
+                                           scales.shape[0], scales.shape[1], _ptr(bias), _ptr(out), out.stride(0),
+                                           flags, _stream(device)))
+    return out
+
+
+def _status_workspace(device):
+    return torch.empty(256, dtype=torch.uint8, device=device)
+
+
+def codec_ocp_to_half(codes, scales):
+    """GPU forward codec on device tensors -> (half codes uint8, 2*scales, rounded) or GkError."""
+    device = require_device(codes.device)
+    src = _u8(codes)
+    dst = torch.empty_like(src)
+    s_out = torch.empty_like(scales)
+    ws = _status_workspace(device)
+    rounded = ctypes.c_int64(0)
+    lib = nat.load()
+    nat.check("gk_fp8_codec_ocp_to_half",
+              lib.gk_fp8_codec_ocp_to_half(_ptr(src), _ptr(dst), src.numel(), _ptr(scales), _ptr(s_out),
+                                           scales.numel(), ctypes.byref(rounded), _ptr(ws), ws.numel(),
+                                           _stream(device)))
+    return dst, s_out, rounded.value
+
+
+def codec_half_to_ocp(codes, scales):
+    """GPU inverse codec on device tensors -> (OCP codes uint8, scales/2) or GkError."""
+    device = require_device(codes.device)
+    src = _u8(codes)
+    dst = torch.empty_like(src)
+    s_out = torch.empty_like(scales)
+    ws = _status_workspace(device)
+    lib = nat.load()
+    nat.check("gk_fp8_codec_half_to_ocp",
+              lib.gk_fp8_codec_half_to_ocp(_ptr(src), _ptr(dst), src.numel(), _ptr(scales), _ptr(s_out),
+                                           scales.numel(), _ptr(ws), ws.numel(), _stream(device)))
+    return dst, s_out
+
+
+def inputs_finite(x, weight, scales):
+    """True iff x is finite, weight holds no OCP NaN code and scales are finite and >= 0 (GPU check)."""
+    device = require_device(x.device)
+    ws = _status_workspace(device)
+    w8 = _u8(weight)
+    lib = nat.load()
+    st = lib.gk_fp8_check_inputs(_ptr(x), x.shape[0], x.shape[1], x.stride(0), _ptr(w8), w8.shape[0],
+                                 _ptr(scales), scales.numel(), _ptr(ws), ws.numel(), _stream(device))
+    if st == nat.GK_NONFINITE_INPUT:
+        return False
+    nat.check("gk_fp8_check_inputs", st)
+    return True

@@ -1,0 +1,50 @@
+"""GPU activation quantization is bit-exact with the oracle (block_fp8_oracle.py:25-28, :31-34)."""
+
+import pytest
+import torch
+
+from gaudi_kernels import ops
+from oracle import block_fp8
+
+pytestmark = pytest.mark.gpu
+
+
+def make_x(m, k, seed, kind):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=gen)
+    if kind == "outliers":
+        cols = torch.randperm(k, generator=gen)[: max(1, k // 100)]
+        x[:, cols] *= 20
+    elif kind == "mixed":
+        x[0, :min(k, 128)] = 0                       # all-zero group
+        if m > 1:
+            x[1] *= 1e-30                            # tiny row (bf16 keeps it)
+        if m > 2:
+            x[2] *= 1e30                             # huge row
+        if m > 3:
+            x[3, ::7] = 0
+    return x.bfloat16()
+
+
+@pytest.mark.parametrize("m,k", [(1, 4096), (16, 4096), (5, 333), (37, 384), (300, 7168), (2, 14336)])
+@pytest.mark.parametrize("kind", ["outliers", "mixed"])
+@pytest.mark.parametrize("native_half", [False, True])
+def test_act_quant_bit_exact(m, k, kind, native_half):
+    x = make_x(m, k, m * 1000 + k, kind)
+    m_pad = m + 3
+    q, sa = ops.act_quant(x.cuda(), native_half=native_half, m_pad=m_pad)
+    want_q, want_sa = block_fp8.act_quant(x, native_half)
+    g = (k + 127) // 128
+    assert q.shape == (m_pad, g * 128) and sa.shape == (m_pad, g)
+    assert torch.equal(q[:m].cpu(), want_q)
+    assert torch.equal(sa[:m].cpu().view(torch.int32), want_sa.contiguous().view(torch.int32))
+    assert int(q[m:].abs().sum()) == 0 and float(sa[m:].abs().sum()) == 0.0
+
+
+def test_strided_rows():
+    x = make_x(8, 1024, 5, "outliers")
+    wide = torch.zeros(8, 1536, dtype=torch.bfloat16)
+    wide[:, :1024] = x
+    q, sa = ops.act_quant(wide.cuda()[:, :1024], m_pad=8)
+    want_q, want_sa = block_fp8.act_quant(x)
+    assert torch.equal(q.cpu(), want_q) and torch.equal(sa.cpu(), want_sa)
