@@ -117,7 +117,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
       wa[u][1] = load_stream16(w8 + 16);
       qb[u][0] = q4[0];
       qb[u][1] = q4[1];
-      f[u] = (g0 + u < gend) ? sap[g] * swp[g] : 0.0f;
+      // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
+      f[u] = (g0 + u < gend) ? sap[g] * (HALF_W ? 2.0f * swp[g] : swp[g]) : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
         qreg[i] = *reinterpret_cast<const uint4*>(qsrc[i] + koff);
       }
     }
-    const float swg = swp[g];
+    const float swg = HALF_W ? 2.0f * swp[g] : swp[g];  // native_half: scales x2
     float f[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) f[j] = sap[j][g] * swg;
@@ -282,7 +283,8 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __rest
       if (half_w) wc = codec_half4(wc) & 0xffu;
       part = fmaf(e4m3_value(qa[m * ldq + k]), e4m3_value(wc), part);
     }
-    acc = fmaf(part, sa[static_cast<int64_t>(m) * G + g] * sw[static_cast<int64_t>(n >> 7) * G + g], acc);
+    const float swg = sw[static_cast<int64_t>(n >> 7) * G + g];
+    acc = fmaf(part, sa[static_cast<int64_t>(m) * G + g] * (half_w ? 2.0f * swg : swg), acc);
   }
   if (bias) acc += bias[n];
   y[static_cast<int64_t>(m) * ldy + n] = bf16_rne(acc);
