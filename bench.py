@@ -100,6 +100,46 @@ def time_loop(fn, iters, warmup):
     return time_graph(capture(fn, iters), iters)
 
 
+def rocprof_summary(directory):
+    """Markdown tables from rocprofv3 csv output: kernel trace durations and PMC counters per dispatch shape.
+
+    Dispatches are grouped by (kernel, grid size): one kernel name covers
+    several GEMM shapes in one bench run.  Counter values are rocprofv3's
+    (KiB per dispatch for FETCH_SIZE / WRITE_SIZE), unscaled.
+    """
+    import csv
+    import glob
+    from collections import defaultdict
+
+    def med(v):
+        v = sorted(v)
+        return v[len(v) // 2]
+
+    for path in sorted(glob.glob(os.path.join(directory, "**", "*_kernel_trace.csv"), recursive=True)):
+        agg = defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            grid = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}"
+            agg[(r["Kernel_Name"].split("(")[0], grid, r["Workgroup_Size_X"])].append(
+                int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        print(f"### kernel trace: {os.path.relpath(path, directory)}\n")
+        print("| kernel | grid (threads) | wg | calls | avg us | median us | min us |")
+        print("|---|---|---|---|---|---|---|")
+        for (name, grid, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+            print(f"| `{name}` | {grid} | {wg} | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {med(v) / 1e3:.2f} | "
+                  f"{min(v) / 1e3:.2f} |")
+        print()
+    for path in sorted(glob.glob(os.path.join(directory, "**", "*_counter_collection.csv"), recursive=True)):
+        agg = defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            agg[(r["Kernel_Name"].split("(")[0], r["Grid_Size"], r["Counter_Name"])].append(float(r["Counter_Value"]))
+        print(f"### counters: {os.path.relpath(path, directory)}\n")
+        print("| kernel | grid (threads) | counter | dispatches | median | min | max |")
+        print("|---|---|---|---|---|---|---|")
+        for (name, grid, ctr), v in sorted(agg.items()):
+            print(f"| `{name}` | {grid} | {ctr} | {len(v)} | {med(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
+        print()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,7 +147,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", choices=["decode", "prefill", "mlp"], default=None)
+    ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
+                    help="print per-kernel, per-grid tables of a rocprofv3 csv output directory and exit")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        rocprof_summary(args.rocprof_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU runs its own shard, "
               "see DESIGN.md); run with --gpus 1", file=sys.stderr)
@@ -175,6 +220,17 @@ def main():
             f"({per_m[str(m)]['gemm_kernel_GBps']} GB/s)")
     del rot
     torch.cuda.empty_cache()
+
+    # Plain device-to-device copy of a known size: the calibration kernel for
+    # the FETCH_SIZE / WRITE_SIZE counters read by `rocprofv3 --pmc` runs of
+    # this script (the counters of the GEMM are scaled by what they read here).
+    copy_bytes = 256 << 20
+    csrc = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
+    cdst = torch.empty_like(csrc)
+    for _ in range(3):
+        cdst.copy_(csrc)
+    torch.cuda.synchronize()
+    del csrc, cdst
 
     b16 = gemm_bytes(16, n, k)
     achieved = b16 / (kernel_us_m16 * 1e-6) / 1e9
