@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void check_inputs_kernel(const uint16_t* __res
 struct Plan {
   int variant;
   int64_t m_pad;
-  size_t q_bytes, sa_bytes;
+  size_t q_bytes = 0, sa_bytes = 0;  // quantized activations [G][m_pad][128] and scales [G][m_pad]
+  gk::DecodeShape dec{0, 0};
 };
 
 gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, Plan* p) {
@@ -107,6 +108,7 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
   const uint32_t force = flags & (GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL | GK_FLAG_FORCE_GENERIC);
   if (force & (force - 1)) return GK_UNSUPPORTED_LAYER_CONFIGURATION;  // more than one forced variant
   const bool tiled_ok = (k % 128 == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
+  const int64_t g = (k + 127) / 128;
   int variant;
   if (force == GK_FLAG_FORCE_GENERIC || (!force && !tiled_ok)) {
     variant = GK_VARIANT_GENERIC;
@@ -120,13 +122,14 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
   } else {
     variant = m <= gk::kDecodeMaxRows ? GK_VARIANT_DECODE : GK_VARIANT_PREFILL;
   }
-  const int64_t g = (k + 127) / 128;
+  *p = Plan();
   p->variant = variant;
-  p->m_pad = variant == GK_VARIANT_DECODE ? gk::kDecodeMaxRows
+  p->m_pad = variant == GK_VARIANT_DECODE    ? gk::kDecodeMaxRows
              : variant == GK_VARIANT_PREFILL ? round_up(m, gk::kPrefillRowTile)
                                              : m;
   p->q_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 128);
   p->sa_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 4);
+  if (variant == GK_VARIANT_DECODE) p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g));
   return GK_SUCCESS;
 }
 
@@ -140,8 +143,8 @@ gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* sc
   return GK_SUCCESS;
 }
 
-gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, int64_t k, const void* w, int64_t n,
-                   const float* scales, const float* bias, void* y, int64_t ldy, uint32_t flags,
+gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, int64_t k, const void* w,
+                   int64_t n, const float* scales, const float* bias, void* y, int64_t ldy, uint32_t flags,
                    hipStream_t stream) {
   gk::GemmArgs a;
   a.qa = q;
@@ -157,6 +160,7 @@ gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, 
   a.G = static_cast<int>((k + 127) / 128);
   a.Mpad = static_cast<int>(p.m_pad);
   a.half_w = (flags & GK_FLAG_NATIVE_HALF) != 0;
+  a.dec = p.dec;
   hipError_t e;
   switch (p.variant) {
     case GK_VARIANT_DECODE: e = gk::launch_gemm_decode(a, stream); break;

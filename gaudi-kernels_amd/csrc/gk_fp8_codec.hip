@@ -13,8 +13,9 @@
 //
 // The activation quantizer restates block_fp8_oracle.py:25-28 (and :31-34 for
 // native_half): per row and 128-column group, sa = fp32(max(amax, 1e-10)) *
-// fp32(1/448), q = e4m3_rne(clamp(fp32(x / sa), +-448)) with an IEEE divide.
-// Sixteen lanes own one group (8 bf16 each, one 16-byte load per lane).
+// fp32(1/448), q = e4m3_rne(clamp(fp32(x / sa), +-448)) -- the exact codes of
+// the IEEE quotient (quant_group8 in gk_fp8_internal.h).  Sixteen lanes own
+// one group (8 bf16 each, one 16-byte load per lane).
 
 #include "gk_fp8_internal.h"
 
@@ -138,9 +139,10 @@ __global__ __launch_bounds__(256) void codec_scales_kernel(const float* __restri
 }
 
 // ---- activation quantizer ----------------------------------------------------
-// x: bf16 [M, K] with row stride ldx (elements).  q: [Mpad, G*128] codes (rows
-// >= M and columns >= K are written as zero), sa: [Mpad, G] fp32 (zero for rows
-// >= M).  One group = 16 lanes x 8 elements.
+// x: bf16 [M, K] with row stride ldx (elements).  Group-major outputs (the
+// reference quant op's {128, R, G} layout): q [G][Mpad][128] codes (rows >= M
+// and columns >= K are written as zero), sa [G][Mpad] fp32 (zero for rows >=
+// M).  One group = 16 lanes x 8 elements (quant_group8).
 template <bool HALF>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                         int K, int G, int Mpad, uint8_t* __restrict__ q,
@@ -152,43 +154,22 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   const int64_t row = active ? gid / G : 0;
   const int g = active ? static_cast<int>(gid - row * G) : 0;
   const int col = g * 128 + sub * 8;
-  float v[8];
-  if (active && row < M && col + 8 <= K && vec_ok) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(x + row * ldx + col);
-    const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+  const bool live = active && row < M;
+  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+  if (live && col + 8 <= K && vec_ok) {
+    raw = *reinterpret_cast<const uint4*>(x + row * ldx + col);
+  } else if (live) {
+    uint32_t h[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = bits_f32(w4[i] << 16);
-      v[2 * i + 1] = bits_f32(w4[i] & 0xffff0000u);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      v[i] = (active && row < M && col + i < K) ? bf16_value(x[row * ldx + col + i]) : 0.0f;
+    for (int i = 0; i < 8; ++i) h[i] = (col + i < K) ? x[row * ldx + col + i] : 0u;
+    raw = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
   }
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
-  // block_fp8_oracle.py:27 -- clamp_min(1e-10) then fp32 multiply by fp32(1/448).
-  const float s = fmaxf(amax, 1e-10f) * (1.0f / 448.0f);
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float t = v[i] / s;                       // IEEE fp32 division (correctly rounded)
-    t = fminf(fmaxf(t, -448.0f), 448.0f);
-    const uint32_t c = e4m3_rne(t);
-    if (i < 4) lo |= c << (8 * i); else hi |= c << (8 * (i - 4));
-  }
-  if (HALF) {  // block_fp8_oracle.py:32,34: e4m3fn(qa * 0.5), sa * 2
-    lo = codec_half4(lo);
-    hi = codec_half4(hi);
-  }
+  float s;
+  const uint2 codes = quant_group8(raw, live, HALF, &s);  // all 16 lanes of a group take part
   if (active) {
-    const bool live = row < M;
-    *reinterpret_cast<uint2*>(q + row * static_cast<int64_t>(G) * 128 + col) = live ? make_uint2(lo, hi) : make_uint2(0u, 0u);
-    if (sub == 0) sa[row * G + g] = live ? (HALF ? s * 2.0f : s) : 0.0f;
+    const int64_t slot = static_cast<int64_t>(g) * Mpad + row;
+    *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = live ? codes : make_uint2(0u, 0u);
+    if (sub == 0) sa[slot] = live ? s : 0.0f;
   }
 }
 

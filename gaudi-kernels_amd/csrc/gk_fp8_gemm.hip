@@ -16,9 +16,13 @@
 // result lands as C[n = 4*(lane/16) + r][m = lane%16], so one lane's four
 // accumulators share one token m and one 128-row weight block: the promotion
 // factor sa[m,g]*sw[nb,g] is a single scalar per lane.  Both operands put the
-// same 32 K-bytes in a lane (K offset 32*(lane/16)); because the hardware
-// pairs A and B bytes by the same (lane, byte) position, the result does not
-// depend on which K indices those bytes are.
+// same 32 K-bytes of the group in a lane; because the hardware pairs A and B
+// bytes by the same (lane, byte) position, the result does not depend on
+// which K indices those bytes are.
+//
+// Quantized activations are group-major, qa [G][Mpad][128] and sa [G][Mpad]
+// (the reference quant op's {128, R, G} layout, generic_fp8_glue.hpp:84-109):
+// the 16 x 128 codes of one group and 16 tokens are one contiguous 2 KB block.
 
 #include "gk_fp8_internal.h"
 
@@ -80,11 +84,19 @@ __device__ inline void store_tile(uint16_t* __restrict__ y, int64_t ldy, const f
 
 // ---------------------------------------------------------------------------
 // Decode variant (M <= 16): HBM-bound weight streaming.
-// One workgroup owns 16 weight rows; its NW waves split the G groups into
-// contiguous ranges and each streams its 16 x (range*128) weight slab with
-// 16-byte loads, U groups in flight per wave.  qa/sa (16 padded rows) are
-// L2-resident.  Wave partials are summed in LDS in fixed wave order.
-template <int NW, int U, bool HALF_W>
+//
+// Workgroup = NW waves over R 16-row weight tiles (16R rows).  The waves split
+// the G groups into contiguous ranges.  Per group a wave loads the 16 x 128
+// activation fragment once (L2-resident, 2 x 16 bytes per lane) and the R
+// weight fragments (the four lanes of a row read 64 contiguous bytes per
+// instruction), then runs R MFMAs: activation traffic is 1/R of the weight
+// traffic.  U groups are loaded per batch so that U*R*2 16-byte weight loads
+// per lane are in flight.  The NW wave partials are summed in LDS in wave
+// order (deterministic) and rounded to bf16 with the bias.
+//
+// Lane chunk pattern (A and B alike): lane (col, quad) holds bytes
+// [16 quad, 16 quad + 16) and [64 + 16 quad, 80 + 16 quad) of the group.
+template <int NW, int R, int U, bool HALF>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -92,52 +104,61 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
                                                               const float* __restrict__ bias,
                                                               uint16_t* __restrict__ y, int64_t ldy, int M,
                                                               int N, int K, int G) {
-  __shared__ v4f red[NW][64];
+  static_assert(16 * R <= 128 && NW >= R, "a workgroup's rows lie in one 128-row scale block");
+  __shared__ v4f red[NW][R][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, quad = lane >> 4;
-  const int n0 = blockIdx.x * 16;
-  const int nrow = min(n0 + col, N - 1);  // rows past N are computed on row N-1 and discarded
-  const int64_t ldq = static_cast<int64_t>(G) * 128;
-  const uint8_t* wp = w + static_cast<int64_t>(nrow) * K + quad * 32;
-  const uint8_t* qp = qa + col * ldq + quad * 32;
-  const float* sap = sa + col * G;
+  const int n0 = blockIdx.x * 16 * R;
+  const uint8_t* wp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    wp[r] = w + static_cast<int64_t>(min(n0 + 16 * r + col, N - 1)) * K + quad * 16;  // rows past N: dropped
+  const uint8_t* qp = qa + col * 128 + quad * 16;   // + g * 2048 (Mpad = 16)
+  const float* sap = sa + col;                      // + g * 16
   const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
 
-  v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   for (int g0 = gbeg; g0 < gend; g0 += U) {
-    uint4 wa[U][2], qb[U][2];
+    uint4 wa[U][R][2], qb[U][2];
     float f[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = min(g0 + u, gend - 1);
-      const uint8_t* w8 = wp + static_cast<int64_t>(g) * 128;
-      const uint4* q4 = reinterpret_cast<const uint4*>(qp + static_cast<int64_t>(g) * 128);
-      wa[u][0] = load_stream16(w8);
-      wa[u][1] = load_stream16(w8 + 16);
-      qb[u][0] = q4[0];
-      qb[u][1] = q4[1];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        wa[u][r][0] = load_stream16(wp[r] + static_cast<int64_t>(g) * 128);
+        wa[u][r][1] = load_stream16(wp[r] + static_cast<int64_t>(g) * 128 + 64);
+      }
+      const uint8_t* q = qp + static_cast<int64_t>(g) * 2048;
+      qb[u][0] = *reinterpret_cast<const uint4*>(q);
+      qb[u][1] = *reinterpret_cast<const uint4*>(q + 64);
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-      f[u] = (g0 + u < gend) ? sap[g] * (HALF_W ? 2.0f * swp[g] : swp[g]) : 0.0f;
+      f[u] = (g0 + u < gend) ? sap[g * 16] * (HALF ? 2.0f * swp[g] : swp[g]) : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const v4f t = mfma_f8(weight_frag<HALF_W>(wa[u][0], wa[u][1]), pack8(qb[u][0], qb[u][1]));
-      acc[0] = fmaf(t[0], f[u], acc[0]);
-      acc[1] = fmaf(t[1], f[u], acc[1]);
-      acc[2] = fmaf(t[2], f[u], acc[2]);
-      acc[3] = fmaf(t[3], f[u], acc[3]);
+      const v8i b = pack8(qb[u][0], qb[u][1]);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const v4f t = mfma_f8(weight_frag<HALF>(wa[u][r][0], wa[u][r][1]), b);
+        acc[r][0] = fmaf(t[0], f[u], acc[r][0]);
+        acc[r][1] = fmaf(t[1], f[u], acc[r][1]);
+        acc[r][2] = fmaf(t[2], f[u], acc[r][2]);
+        acc[r][3] = fmaf(t[3], f[u], acc[r][3]);
+      }
     }
   }
-  if (NW > 1) {
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;
-    acc = red[0][lane];
 #pragma unroll
-    for (int v = 1; v < NW; ++v) acc += red[v][lane];
-  }
-  store_tile(y, ldy, bias, M, N, col, n0 + 4 * quad, acc);
+  for (int r = 0; r < R; ++r) red[wave][r][lane] = acc[r];
+  __syncthreads();
+  if (wave >= R) return;
+  v4f sum = red[0][wave][lane];
+#pragma unroll
+  for (int v = 1; v < NW; ++v) sum += red[v][wave][lane];
+  store_tile(y, ldy, bias, M, N, col, n0 + 16 * wave + 4 * quad, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -157,12 +178,12 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
                                                            const float* __restrict__ sw,
                                                            const float* __restrict__ bias,
                                                            uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                           int K, int G) {
+                                                           int K, int G, int Mpad) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][kPB * kPB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   const int n0 = blockIdx.x * kPB, m0 = blockIdx.y * kPB;
-  const int64_t ldq = static_cast<int64_t>(G) * 128;
+  const int64_t qstep = static_cast<int64_t>(Mpad) * 128;  // one group of qa [G][Mpad][128]
 
   // Global -> LDS staging: chunk c = tid + 256 i, row = c / 8, 16-byte chunk = c % 8.
   const int lrow = tid >> 3, lkc = tid & 7;
@@ -173,7 +194,7 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
   for (int i = 0; i < 4; ++i) {
     const int r = lrow + 32 * i;
     wsrc[i] = w + static_cast<int64_t>(min(n0 + r, N - 1)) * K + lkc * 16;
-    qsrc[i] = qa + static_cast<int64_t>(m0 + r) * ldq + lkc * 16;
+    qsrc[i] = qa + static_cast<int64_t>(m0 + r) * 128 + lkc * 16;
     soff[i] = swz(r, lkc);
   }
   // Fragment reads.
@@ -187,7 +208,7 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
   }
   const float* sap[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sap[j] = sa + static_cast<int64_t>(m0 + wm * 64 + j * 16 + fr) * G;
+  for (int j = 0; j < 4; ++j) sap[j] = sa + (m0 + wm * 64 + j * 16 + fr);  // + g * Mpad
   const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
 
   v4f acc[4][4];
@@ -216,13 +237,13 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         wreg[i] = *reinterpret_cast<const uint4*>(wsrc[i] + koff);
-        qreg[i] = *reinterpret_cast<const uint4*>(qsrc[i] + koff);
+        qreg[i] = *reinterpret_cast<const uint4*>(qsrc[i] + (g + 1) * qstep);
       }
     }
     const float swg = HALF_W ? 2.0f * swp[g] : swp[g];  // native_half: scales x2
     float f[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f[j] = sap[j][g] * swg;
+    for (int j = 0; j < 4; ++j) f[j] = sap[j][static_cast<int64_t>(g) * Mpad] * swg;
     v8i bfr[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -268,11 +289,10 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __rest
                                                            const float* __restrict__ sw,
                                                            const float* __restrict__ bias,
                                                            uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                           int K, int G, int half_w) {
+                                                           int K, int G, int Mpad, int half_w) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= static_cast<int64_t>(M) * N) return;
   const int m = static_cast<int>(idx / N), n = static_cast<int>(idx % N);
-  const int64_t ldq = static_cast<int64_t>(G) * 128;
   float acc = 0.0f;
   for (int g = 0; g < G; ++g) {
     float part = 0.0f;
@@ -281,36 +301,65 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __rest
       const int64_t k = static_cast<int64_t>(g) * 128 + i;
       uint32_t wc = w[static_cast<int64_t>(n) * K + k];
       if (half_w) wc = codec_half4(wc) & 0xffu;
-      part = fmaf(e4m3_value(qa[m * ldq + k]), e4m3_value(wc), part);
+      part = fmaf(e4m3_value(qa[(static_cast<int64_t>(g) * Mpad + m) * 128 + i]), e4m3_value(wc), part);
     }
     const float swg = sw[static_cast<int64_t>(n >> 7) * G + g];
-    acc = fmaf(part, sa[static_cast<int64_t>(m) * G + g] * (half_w ? 2.0f * swg : swg), acc);
+    acc = fmaf(part, sa[static_cast<int64_t>(g) * Mpad + m] * (half_w ? 2.0f * swg : swg), acc);
   }
   if (bias) acc += bias[n];
   y[static_cast<int64_t>(m) * ldy + n] = bf16_rne(acc);
 }
 
 // ---------------------------------------------------------------------------
-hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
-  constexpr int NW = 4, U = 8;
-  const dim3 grid((a.N + 15) / 16);
+template <int NW, int R, int U>
+static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
   if (a.half_w)
-    gemm_decode_kernel<NW, U, true><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
-                                                                   a.M, a.N, a.K, a.G);
+    gemm_decode_kernel<NW, R, U, true><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
+                                                                      a.M, a.N, a.K, a.G);
   else
-    gemm_decode_kernel<NW, U, false><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
-                                                                    a.M, a.N, a.K, a.G);
+    gemm_decode_kernel<NW, R, U, false><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
+                                                                       a.M, a.N, a.K, a.G);
   return hipGetLastError();
+}
+
+DecodeShape plan_decode_shape(int N, int G) {
+  // R: 16-row tiles per workgroup -- larger R cuts activation traffic (1/R of
+  // the weights) but leaves fewer workgroups; keep >= 192 of them for 256 CUs.
+  const int tiles = (N + 15) / 16;
+  const int r = tiles >= 4 * 384 ? 4 : tiles >= 2 * 192 ? 2 : 1;
+  const int wgs = (tiles + r - 1) / r;
+  // NW: waves per workgroup splitting K, for ~3072 waves in flight (12 per CU).
+  int nw = 4;
+  while (nw < 16 && wgs * nw * 2 <= 3072) nw *= 2;
+  (void)G;
+  return DecodeShape{nw, r};
+}
+
+hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
+  const int key = a.dec.nw * 10 + a.dec.r;
+  switch (key) {
+    case 41: return decode_launch<4, 1, 4>(a, stream);
+    case 42: return decode_launch<4, 2, 4>(a, stream);
+    case 44: return decode_launch<4, 4, 4>(a, stream);
+    case 81: return decode_launch<8, 1, 4>(a, stream);
+    case 82: return decode_launch<8, 2, 4>(a, stream);
+    case 84: return decode_launch<8, 4, 2>(a, stream);
+    case 161: return decode_launch<16, 1, 2>(a, stream);
+    case 162: return decode_launch<16, 2, 2>(a, stream);
+    case 164: return decode_launch<16, 4, 1>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid((a.N + kPB - 1) / kPB, (a.M + kPB - 1) / kPB);
   if (a.half_w)
     gemm_prefill_kernel<true><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,
-                                                        a.K, a.G);
+                                                        a.K, a.G, a.Mpad);
   else
     gemm_prefill_kernel<false><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,
-                                                         a.K, a.G);
+                                                         a.K, a.G, a.Mpad);
   return hipGetLastError();
 }
 
@@ -318,7 +367,7 @@ hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream) {
   const int64_t total = static_cast<int64_t>(a.M) * a.N;
   const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   gemm_generic_kernel<<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G,
-                                                a.half_w ? 1 : 0);
+                                                a.Mpad, a.half_w ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -17,6 +17,46 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kDecodeMaxRows = 16;   // decode variant: M <= 16, padded to one MFMA column tile
 constexpr int kPrefillRowTile = 256; // prefill variant: M padded to the token tile
 
+// ---- 1x128 activation quantizer (block_fp8_oracle.py:25-28, :32,:34) -------
+// Sixteen consecutive lanes own one 128-element group, 8 bf16 each (one
+// 16-byte load).  Returns the lane's 8 OCP E4M3 codes (byte i = element i)
+// and writes the group's scale (x2 in native_half mode).  amax is reduced
+// over the 16 lanes with xor shuffles; the fp32 quotient is act_quotient
+// (exact E4M3 codes of the IEEE quotient); the encode is the gfx950
+// v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN), which equals
+// e4m3_rne for every |v| <= 464 -- and |x / s| < 464 always holds because
+// s >= amax/448 up to two fp32 roundings.
+__device__ inline uint2 quant_group8(uint4 raw, bool live, bool half, float* scale_out) {
+  float v[8];
+  const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = live ? bits_f32(w4[i] << 16) : 0.0f;
+    v[2 * i + 1] = live ? bits_f32(w4[i] & 0xffff0000u) : 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  const float s = act_scale(amax);
+  const float r = 1.0f / s;  // IEEE division, once per lane
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = act_quotient(v[i], s, r);
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+  uint2 codes = make_uint2(static_cast<uint32_t>(lo), static_cast<uint32_t>(hi));
+  if (half) {  // block_fp8_oracle.py:32,34: e4m3fn(qa * 0.5), sa * 2
+    codes.x = codec_half4(codes.x);
+    codes.y = codec_half4(codes.y);
+  }
+  *scale_out = half ? s * 2.0f : s;
+  return codes;
+}
+
 hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t n, const float* scales,
                         float* scales_out, int64_t n_scales, uint32_t* flags, unsigned long long* rounded,
                         hipStream_t stream);
@@ -24,7 +64,14 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
                             bool half, hipStream_t stream);
 
-// Quantized activations qa [Mpad, G*128] / sa [Mpad, G] (from launch_act_quant)
+// Decode variant shape: NW waves per workgroup (splitting K), R 16-row weight
+// tiles per workgroup.  Chosen by plan_decode_shape.
+struct DecodeShape {
+  int nw, r;
+};
+DecodeShape plan_decode_shape(int N, int G);
+
+// Quantized activations qa [G][Mpad][128] / sa [G][Mpad] (launch_act_quant)
 // times weight codes w [N, K] with block scales sw [ceil(N/128), G].
 struct GemmArgs {
   const uint8_t* qa;
@@ -35,8 +82,9 @@ struct GemmArgs {
   uint16_t* y;        // bf16 [M, ldy]
   int64_t ldy;
   int M, N, K, G;
-  int Mpad;
-  bool half_w;        // apply the half-range codec to weight codes in-kernel (native_half)
+  int Mpad;           // 16 for the decode variant
+  bool half_w;        // native_half: half-range codec on weight codes in-kernel, weight scales x2
+  DecodeShape dec;    // decode variant only
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);

@@ -60,6 +60,31 @@ def plan(m, n, k, flags=0, weight=None):
     return variant.value, m_pad.value, ws.value
 
 
+_WORKSPACES = {}
+
+
+def workspace(nbytes, device=None):
+    """A GEMM workspace of at least `nbytes` for the current stream of `device`.
+
+    Cached per (device, stream) and grown on demand, so that calls ordered on
+    one stream reuse it without allocating; GEMMs running on several streams
+    at once get one workspace per stream.
+    """
+    device = require_device(device)
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def make_workspace(m, n, k, *, native_half=False, variant=None, device=None):
+    """A new workspace sized for one (m, n, k, flags) plan; for callers that manage their own."""
+    _, _, nbytes = plan(m, n, k, _flags(native_half, variant))
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=require_device(device))
+
+
 def _flags(native_half, variant):
     flags = nat.GK_FLAG_NATIVE_HALF if native_half else 0
     if variant is not None:
@@ -69,15 +94,18 @@ def _flags(native_half, variant):
 
 
 def act_quant(x, *, native_half=False, m_pad=None):
-    """1x128 activation quantization on the GPU -> (codes uint8 [m_pad, G*128], sa fp32 [m_pad, G])."""
+    """1x128 activation quantization on the GPU -> group-major (codes uint8 [G, m_pad, 128], sa fp32 [G, m_pad]).
+
+    The layout of the reference's quant op output ({128, R, G} FCD-first, generic_fp8_glue.hpp:84-109).
+    """
     device = require_device(x.device)
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
         raise ValueError("expected a 2-D bf16 activation with unit column stride")
     m, k = x.shape
     g = (k + 127) // 128
     m_pad = m if m_pad is None else m_pad
-    q = torch.empty((m_pad, g * 128), dtype=torch.uint8, device=device)
-    sa = torch.empty((m_pad, g), dtype=torch.float32, device=device)
+    q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
+    sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
     lib = nat.load()
     nat.check("gk_fp8_act_quant_bf16",
               lib.gk_fp8_act_quant_bf16(_ptr(x), m, k, x.stride(0), _ptr(q), _ptr(sa), m_pad,
@@ -100,8 +128,9 @@ def block_fp8_gemm(x, weight, scales, bias=None, *, native_half=False, variant=N
     """y = block-FP8 W8A8 linear of bf16 x [M, K] with E4M3 weight [N, K] -> bf16 [M, N] (asynchronous).
 
     variant: None (dispatch by M), "decode", "prefill" or "generic".
-    workspace: optional uint8 device tensor of at least plan(...)[2] + 256 bytes (reused across calls;
-    calls that share one workspace must be ordered on one stream).
+    workspace: optional 256-byte aligned uint8 device tensor of at least plan(...)[2] bytes
+    (make_workspace); calls that share one workspace must be ordered on one stream.  Default: the
+    cached per-stream workspace().
     """
     device = require_device(x.device)
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
@@ -114,12 +143,7 @@ def block_fp8_gemm(x, weight, scales, bias=None, *, native_half=False, variant=N
     flags = _flags(native_half, variant)
     w8 = _u8(weight)
     _, _, ws_bytes = plan(m, n, k, flags, w8)
-    ws = workspace
-    if ws is None or ws.numel() < ws_bytes + 256:
-        if ws is not None:
-            raise ValueError(f"workspace too small: need {ws_bytes + 256} bytes")
-        ws = torch.empty(max(ws_bytes, 256) + 256, dtype=torch.uint8, device=device)
-    ws_ptr = (ws.data_ptr() + 255) // 256 * 256
+    ws = _checked_workspace(workspace, ws_bytes, device)
     if out is None:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
     elif out.dtype != torch.bfloat16 or out.shape != (m, n) or out.stride(1) != 1 or out.device != device:
@@ -128,23 +152,33 @@ def block_fp8_gemm(x, weight, scales, bias=None, *, native_half=False, variant=N
     nat.check("gk_fp8_block_gemm_bf16",
               lib.gk_fp8_block_gemm_bf16(_ptr(x), m, k, x.stride(0), _ptr(w8), n, _ptr(scales), scales.shape[0],
                                          scales.shape[1], _ptr(bias), _ptr(out), out.stride(0), flags,
-                                         ctypes.c_void_p(ws_ptr), ws.numel() - (ws_ptr - ws.data_ptr()),
-                                         _stream(device)))
+                                         _ptr(ws), ws.numel(), _stream(device)))
     return out
 
 
+def _checked_workspace(ws, nbytes, device):
+    if ws is None:
+        return workspace(nbytes, device)
+    if ws.dtype != torch.uint8 or ws.device != device or ws.numel() < nbytes or ws.data_ptr() % 256:
+        raise ValueError(f"workspace must be a 256-byte aligned uint8 tensor of >= {nbytes} bytes on {device}")
+    return ws
+
+
 def block_fp8_gemm_q(q, sa, m, weight, scales, bias=None, *, native_half=False, variant=None, out=None):
-    """GEMM on activations already quantized by act_quant(m_pad=plan(...)[1])."""
+    """GEMM on activations already quantized by act_quant(m_pad=plan(...)[1]) (group-major q, sa)."""
     device = require_device(q.device)
     _check_gemm_operands(weight, scales, bias, device)
     n, k = weight.shape
     flags = _flags(native_half, variant)
     w8 = _u8(weight)
+    g = (k + 127) // 128
+    if q.shape != (g, q.shape[1], 128) or sa.shape != (g, q.shape[1]) or not (q.is_contiguous() and sa.is_contiguous()):
+        raise ValueError("expected group-major q [G, m_pad, 128] and sa [G, m_pad] from act_quant")
     if out is None:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
     lib = nat.load()
     nat.check("gk_fp8_block_gemm_q_bf16",
-              lib.gk_fp8_block_gemm_q_bf16(_ptr(q), _ptr(sa), m, q.shape[0], k, _ptr(w8), n, _ptr(scales),
+              lib.gk_fp8_block_gemm_q_bf16(_ptr(q), _ptr(sa), m, q.shape[1], k, _ptr(w8), n, _ptr(scales),
                                            scales.shape[0], scales.shape[1], _ptr(bias), _ptr(out), out.stride(0),
                                            flags, _stream(device)))
     return out

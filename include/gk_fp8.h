@@ -12,7 +12,9 @@
  *   - Every buffer is caller-owned device memory (HIP); the library never
  *     allocates.  Scratch space is passed as a workspace whose size is asked
  *     for first (two-phase protocol, as the glue's ELF-size query in
- *     csrc/host/generic_attention_glue.hpp:84-90).
+ *     csrc/host/generic_attention_glue.hpp:84-90).  A GEMM workspace is
+ *     256-byte aligned; calls that share a workspace must be ordered (one
+ *     stream).
  *   - `stream` is a hipStream_t passed as void* (NULL = default stream).  All
  *     entry points are stream-ordered and asynchronous, except the codec and
  *     gk_fp8_check_inputs, which read a status word back and synchronize the
@@ -105,9 +107,9 @@ gk_status gk_fp8_codec_half_to_ocp(const void* src, void* dst, int64_t n, const 
 /* Per-row 1x128 E4M3 quantization with the oracle's scale rule
  * (block_fp8_oracle.py:25-28; native_half adds :32,:34).  Replaces the
  * gk_fp8_block_quant_bf16_v1 op (activation_native.c:9-30, glue
- * generic_fp8_glue.hpp:84-109), in the row-major layout the GEMM consumes:
- * q codes [m_pad, G*128] (G = ceil(k/128)), sa fp32 [m_pad, G]; rows >= m
- * and columns >= k are written as zero.  m_pad >= m. */
+ * generic_fp8_glue.hpp:84-109) in that op's group-major layout ({128, R, G}
+ * FCD-first): q codes [G][m_pad][128] (G = ceil(k/128)), sa fp32 [G][m_pad];
+ * rows >= m and columns >= k are written as zero.  m_pad >= m. */
 gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, void* q, float* sa,
                                 int64_t m_pad, uint32_t flags, void* stream);
 
@@ -125,7 +127,7 @@ gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags
  * act_row_scale -> quant_act_fp16_1k -> dequant_weight_fp16_1k -> MME ->
  * epilogue(_bias) (fp8_hybrid_tpcsim_test.cpp:180-324).  Dispatch by M:
  * M <= 16 streams weights (decode), larger M runs the LDS-tiled MFMA kernel
- * (prefill).  scale_rows x scale_cols must equal ceil(n/128) x ceil(k/128)
+ * (prefill).  The activations are quantized into the workspace first.  scale_rows x scale_cols must equal ceil(n/128) x ceil(k/128)
  * (GK_INCOMPATIBLE_INPUT_SIZE otherwise, as generic_fp8_glue_test.cpp:98-100).
  * bias may be NULL.  Inputs are not checked for NaN (see gk_fp8_check_inputs). */
 gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
@@ -134,7 +136,7 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
                                  void* stream);
 
 /* The same GEMM on activations already quantized by gk_fp8_act_quant_bf16
- * (q [m_pad, G*128], sa [m_pad, G]); m_pad must equal the plan's m_pad for
+ * (q [G][m_pad][128], sa [G][m_pad]); m_pad must equal the plan's m_pad for
  * these flags.  No workspace.  (The second half of the Gaudi2 decode chain:
  * MME partials + reduce_bias.c, fused.) */
 gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, int64_t m_pad, int64_t k,

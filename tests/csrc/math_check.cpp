@@ -2,8 +2,38 @@
 // gfx950 kernels run), exposed with a C ABI so tests can sweep it against
 // the CPU oracle.  Built by tests/test_math_host.py with g++.
 #include <stdint.h>
+#include <string.h>
+
+#include <thread>
+#include <vector>
 
 #include "gk_fp8_math.h"
+
+namespace {
+
+float bf16_bits_to_f32(uint32_t h) { return gk::bits_f32(h << 16); }
+
+// Mismatching e4m3 codes between gk::act_quotient and IEEE division, for
+// amax over the bf16 magnitudes amax_lo <= a < amax_hi (step `step`) and
+// every finite bf16 x with |x| <= a.
+int64_t div_mismatches_range(uint32_t a_first, uint32_t a_step, uint32_t a_end) {
+  int64_t bad = 0;
+  for (uint32_t ah = a_first; ah < a_end; ah += a_step) {
+    const float s = gk::act_scale(bf16_bits_to_f32(ah));
+    volatile float one = 1.0f;
+    const float r = one / s;
+    for (uint32_t xh = 0; xh < 0x10000u; ++xh) {
+      if ((xh & 0x7fffu) > ah) continue;
+      const float x = bf16_bits_to_f32(xh);
+      volatile float vx = x;
+      const float ieee = vx / s;
+      if (gk::e4m3_rne(gk::act_quotient(x, s, r)) != gk::e4m3_rne(ieee)) ++bad;
+    }
+  }
+  return bad;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -30,6 +60,22 @@ void mc_swar(int op, const uint32_t* x, uint32_t* out, int64_t n) {
       default: out[i] = gk::half_invalid4(x[i]); break;
     }
   }
+}
+
+// Exhaustive check of the quantizer's division (gk::act_quotient): every
+// finite positive bf16 amax (and zero, which the 1e-10 clamp covers) and
+// every finite bf16 x with |x| <= amax.  Returns the number of mismatching
+// E4M3 codes against IEEE fp32 division followed by the same encoder.
+int64_t mc_div_mismatches(int threads) {
+  if (threads < 1) threads = 1;
+  std::vector<int64_t> bad(threads, 0);
+  std::vector<std::thread> pool;
+  for (int t = 0; t < threads; ++t)
+    pool.emplace_back([t, threads, &bad] { bad[t] = div_mismatches_range(t, threads, 0x7f80u); });
+  for (auto& th : pool) th.join();
+  int64_t total = 0;
+  for (int64_t b : bad) total += b;
+  return total;
 }
 
 }  // extern "C"

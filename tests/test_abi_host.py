@@ -54,6 +54,7 @@ def test_load_version_and_ops():
 def test_plan_dispatch_by_m():
     for m in (1, 2, 4, 8, 16):
         v, mp, ws = ops.plan(m, 6144, 4096)
+        # quantized-activation scratch: 16 x 4096 codes + 16 x 32 scales
         assert v == nat.GK_VARIANT_DECODE and mp == 16 and ws == 16 * 4096 + 16 * 32 * 4
     v, mp, ws = ops.plan(17, 6144, 4096)
     assert v == nat.GK_VARIANT_PREFILL and mp == 256

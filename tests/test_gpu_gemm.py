@@ -151,6 +151,35 @@ def test_q_entry_point_matches_fused():
     for variant in ("decode", "prefill"):
         _, m_pad, _ = ops.plan(m, n, k, {"decode": 2, "prefill": 4}[variant])
         q, sa = ops.act_quant(x, m_pad=m_pad)
-        y1 = ops.block_fp8_gemm_q(q, sa, m, w.cuda(), s.cuda(), variant=variant)
+        y1 = ops.block_fp8_gemm_q(q, sa, m, w.cuda(), s.cuda(), variant=variant)  # decode: pre-quantized path
         y2 = ops.block_fp8_gemm(x, w.cuda(), s.cuda(), variant=variant)
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 6144, 4096), (5, 4096, 14336), (1, 200, 1024), (16, 64, 128),
+                                   (7, 1000, 3072), (2, 28672, 512), (16, 16, 256)])
+def test_decode_shapes_deterministic(m, n, k):
+    """Every decode workgroup shape the planner picks (R = 1, 2, 4 row tiles; 4-16 waves splitting K; ragged N)
+    matches the oracle and reruns bit-identically (fixed-order wave reduction)."""
+    w, s = synth.weight(n, k, seed=n + k)
+    x = synth.activations(m, k, seed=m + 11).cuda()
+    wd, sd = w.cuda(), s.cuda()
+    y1 = ops.block_fp8_gemm(x, wd, sd)
+    y2 = ops.block_fp8_gemm(x, wd, sd)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), (m, n, k)
+    assert_parity(y1.cpu(), block_fp8.reference(x.cpu(), w, s), f"{m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("native_half", [False, True])
+def test_decode_strided_unaligned_activations(native_half):
+    """x that is not 16-byte aligned (odd row stride) gives the same bits as a dense copy."""
+    m, n, k = 9, 384, 1024
+    w, s = synth.weight(n, k, seed=21)
+    x = synth.activations(m, k, seed=22)
+    base = torch.zeros((m, k + 1), dtype=torch.bfloat16)
+    base[:, 1:] = x
+    xs = base.cuda()[:, 1:]          # row stride k + 1, data pointer offset by 2 bytes
+    y_strided = ops.block_fp8_gemm(xs, w.cuda(), s.cuda(), native_half=native_half, variant="decode")
+    y_dense = ops.block_fp8_gemm(x.cuda(), w.cuda(), s.cuda(), native_half=native_half, variant="decode")
+    assert torch.equal(y_strided.view(torch.int16), y_dense.view(torch.int16))
+    assert_parity(y_dense.cpu(), block_fp8.reference(x, w, s, native_half=native_half))

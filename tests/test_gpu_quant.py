@@ -35,10 +35,12 @@ def test_act_quant_bit_exact(m, k, kind, native_half):
     q, sa = ops.act_quant(x.cuda(), native_half=native_half, m_pad=m_pad)
     want_q, want_sa = block_fp8.act_quant(x, native_half)
     g = (k + 127) // 128
-    assert q.shape == (m_pad, g * 128) and sa.shape == (m_pad, g)
-    assert torch.equal(q[:m].cpu(), want_q)
-    assert torch.equal(sa[:m].cpu().view(torch.int32), want_sa.contiguous().view(torch.int32))
-    assert int(q[m:].abs().sum()) == 0 and float(sa[m:].abs().sum()) == 0.0
+    assert q.shape == (g, m_pad, 128) and sa.shape == (g, m_pad)    # group-major
+    q_rows = q.permute(1, 0, 2).reshape(m_pad, g * 128).cpu()
+    sa_rows = sa.t().cpu()
+    assert torch.equal(q_rows[:m], want_q)
+    assert torch.equal(sa_rows[:m].contiguous().view(torch.int32), want_sa.contiguous().view(torch.int32))
+    assert int(q_rows[m:].abs().sum()) == 0 and float(sa_rows[m:].abs().sum()) == 0.0
 
 
 def test_strided_rows():
@@ -47,4 +49,4 @@ def test_strided_rows():
     wide[:, :1024] = x
     q, sa = ops.act_quant(wide.cuda()[:, :1024], m_pad=8)
     want_q, want_sa = block_fp8.act_quant(x)
-    assert torch.equal(q.cpu(), want_q) and torch.equal(sa.cpu(), want_sa)
+    assert torch.equal(q.permute(1, 0, 2).reshape(8, 1024).cpu(), want_q) and torch.equal(sa.t().cpu(), want_sa)

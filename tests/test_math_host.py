@@ -26,7 +26,7 @@ def mc():
     os.makedirs(BUILD, exist_ok=True)
     so = os.path.join(BUILD, "libmath_check.so")
     src = os.path.join(ROOT, "tests", "csrc", "math_check.cpp")
-    subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC",
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-pthread", "-shared", "-fPIC",
                     "-I", os.path.join(ROOT, "gaudi-kernels_amd", "csrc"), src, "-o", so], check=True)
     lib = ctypes.CDLL(so)
     return lib
@@ -112,3 +112,9 @@ def test_swar_codec_all_bytes_all_lanes(mc):
             assert np.array_equal(got_inv[valid], inv[b][valid])
             bad = swar(mc, 4, words).view(np.uint8).reshape(256, 4)
             assert np.array_equal(bad, np.where(valid, 0, 0x80).astype(np.uint8))
+
+
+def test_quantizer_division_exhaustive(mc):
+    """gk::act_quotient gives the IEEE-division E4M3 code for every bf16 x and bf16 amax >= |x| (2^31 pairs)."""
+    mc.mc_div_mismatches.restype = ctypes.c_int64
+    assert mc.mc_div_mismatches(ctypes.c_int(min(8, os.cpu_count() or 1))) == 0
