@@ -88,7 +88,8 @@ struct GemmArgs {
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
-hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);     // dispatches by M
+hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream);  // 256 x 256 tiles, Mpad % 256 == 0
 hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream);
 
 // Grouped (MoE) variant: rows of qa are sorted by expert; expert e owns rows

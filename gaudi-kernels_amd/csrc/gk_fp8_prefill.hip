@@ -1,0 +1,209 @@
+// Large-M prefill block-FP8 GEMM for gfx950: 256 x 256 output tile per
+// workgroup, FP8 MFMA 32x32x64, per-128-K-group fp32 scale promotion.
+//
+// Same arithmetic as the other variants (block_fp8_oracle.py:38-46): each
+// 128-K group's exact fp8 x fp8 partial (two chained MFMAs over K = 64) is
+// multiplied by sa[m, g] * sw[n / 128, g] and accumulated in fp32; bias and
+// bf16 rounding happen in the epilogue.
+//
+// Structure (one workgroup = 8 waves, 4 along N x 2 along M, 64 x 128 each):
+//   * Stage = one 128-K group: the 256 x 128-byte weight tile and the 256 x
+//     128-byte activation tile, copied global -> LDS with direct-to-LDS loads
+//     (global_load_lds_dwordx4: each wave instruction moves 8 rows x 128 B).
+//     Two stages ping-pong; stage g+1 is loaded while stage g is computed.
+//   * LDS rows are 128 bytes with the 16-byte chunk c of row r stored at slot
+//     c ^ ((r >> 1) & 7): sixteen consecutive rows reading one chunk hit 16
+//     distinct 16-byte bank groups (measured: zero LDS bank conflicts).
+//   * Fragment reads are issued as inline-asm ds_read_b128 with explicit
+//     lgkmcnt waits tied to the fragment registers.  The compiler then does
+//     not treat them as reads that may alias the in-flight direct-to-LDS
+//     loads of the next stage (it would otherwise wait for those loads before
+//     every fragment read and serialize the pipeline).
+//   * 32x32 output layout: lane l, register r -> n = 8 (r/4) + 4 (l/32) + r%4,
+//     m = l % 32: one token per lane, so the promotion factor is one scalar.
+
+#include <mutex>
+
+#include "gk_fp8_tile.h"
+
+namespace gk {
+
+namespace {
+
+constexpr int kBN = 256, kBM = 256;        // workgroup tile (weight rows x tokens)
+constexpr int kTile = 256 * 128;           // one operand tile of one group in LDS
+constexpr int kStageBytes = 2 * kTile;     // weights + activations
+constexpr int kLdsBytes = 2 * kStageBytes; // two stages: 128 KB of the 160 KB LDS
+
+__device__ inline u32x4 lds_read16(uint32_t addr) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+
+__device__ inline v8i lds_frag(uint32_t a0, uint32_t a1) {
+  const u32x4 lo = lds_read16(a0), hi = lds_read16(a1);
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+__device__ inline v8i half_codes(v8i v) {  // native_half: OCP codes -> value / 2 (codec_half4)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = static_cast<int>(codec_half4(static_cast<uint32_t>(v[i])));
+  return v;
+}
+
+__device__ inline void promote(v16f& acc, const v16f& t, float f) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = fmaf(t[r], f, acc[r]);
+}
+
+template <bool HALF>
+__global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
+                                                              const float* __restrict__ sa,
+                                                              const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ sw,
+                                                              const float* __restrict__ bias,
+                                                              uint16_t* __restrict__ y, int64_t ldy, int M, int N,
+                                                              int K, int G, int Mpad) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave & 3, wm = wave >> 2;
+  const int tiles_m = Mpad / kBM;
+  const int tn = static_cast<int>(blockIdx.x) / tiles_m, tm = static_cast<int>(blockIdx.x) % tiles_m;
+  const int n0 = tn * kBN, m0 = tm * kBM;  // consecutive workgroups share the weight panel
+  const int64_t qstep = static_cast<int64_t>(Mpad) * 128;
+
+  // Loader: wave w fills weight rows and activation rows [32 w, 32 w + 32) of
+  // the stage, 4 + 4 instructions of 8 rows; lane -> (row r0 + 8 i, slot ls)
+  // fetches chunk ls ^ key(row).  Weight rows past N re-read row N-1.
+  const int lr = lane >> 3, ls = lane & 7;
+  const int r0 = wave * 32 + lr;
+  int lcs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ (((r0 + 8 * i) >> 1) & 7)) * 16;
+  const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;
+  const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * 128;
+  const int nmax = N - 1 - n0;
+  auto issue = [&](int g, int stage) {
+    uint8_t* base = smem + stage * kStageBytes + wave * 32 * 128;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = min(r0 + 8 * i, nmax);
+      __builtin_amdgcn_global_load_lds(asrc + static_cast<int64_t>(r) * K + static_cast<int64_t>(g) * 128 + lcs[i],
+                                       base + i * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(bsrc + static_cast<int64_t>(r0 + 8 * i) * 128 + g * qstep + lcs[i],
+                                       base + kTile + i * 1024, 16, 0, 0);
+    }
+  };
+
+  // Fragments: lane -> row (lane & 31) of a 32-row strip, chunks h*4 + 2 (lane >> 5) + {0, 1}.
+  const int fr = lane & 31, fc = (lane >> 5) * 2, kf = (fr >> 1) & 7;
+  const uint32_t xo00 = ((0 + fc) ^ kf) << 4, xo01 = ((1 + fc) ^ kf) << 4;
+  const uint32_t xo10 = ((4 + fc) ^ kf) << 4, xo11 = ((5 + fc) ^ kf) << 4;
+  const uint32_t lbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const uint32_t arow = (wn * 64 + fr) * 128, brow = kTile + (wm * 128 + fr) * 128;
+  const float* sap = sa + (m0 + wm * 128 + fr);  // + 32 j + g * Mpad  (m0 + 256 <= Mpad)
+  const float* swp = sw + static_cast<int64_t>(min(n0 + wn * 64, N - 1) >> 7) * G;
+
+  v16f acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  issue(0, 0);
+  for (int g = 0; g < G; ++g) {
+    const int stage = g & 1;
+    float sav[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sav[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
+    // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
+    const float swg = HALF ? 2.0f * swp[g] : swp[g];
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of stage g (and everything older) are done
+    __syncthreads();                // ... for every wave; all reads of stage g-1 are done too
+    if (g + 1 < G) issue(g + 1, stage ^ 1);
+    const uint32_t A = lbase + stage * kStageBytes + arow;
+    const uint32_t B = lbase + stage * kStageBytes + brow;
+    v8i a00 = lds_frag(A + xo00, A + xo01), a01 = lds_frag(A + xo10, A + xo11);
+    v8i a10 = lds_frag(A + 4096 + xo00, A + 4096 + xo01), a11 = lds_frag(A + 4096 + xo10, A + 4096 + xo11);
+    v8i b0 = lds_frag(B + xo00, B + xo01), b1 = lds_frag(B + xo10, B + xo11);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a00), "+v"(a01), "+v"(a10), "+v"(a11), "+v"(b0), "+v"(b1));
+    if (HALF) {
+      a00 = half_codes(a00); a01 = half_codes(a01); a10 = half_codes(a10); a11 = half_codes(a11);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j > 0) {
+        b0 = lds_frag(B + j * 4096 + xo00, B + j * 4096 + xo01);
+        b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
+      }
+      const float f = sav[j] * swg;
+      v16f t0, t1;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { t0[r] = 0.0f; t1[r] = 0.0f; }
+      t0 = mfma32_f8(a00, b0, t0);
+      t1 = mfma32_f8(a10, b0, t1);
+      t0 = mfma32_f8(a01, b1, t0);
+      t1 = mfma32_f8(a11, b1, t1);
+      promote(acc[0][j], t0, f);
+      promote(acc[1][j], t1, f);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        store_tile(y, ldy, bias, M, N, m0 + wm * 128 + j * 32 + fr, n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5),
+                   v);
+      }
+}
+
+// The 128 KB of dynamic LDS is above the default limit: raise it once per device.
+constexpr int kMaxDevices = 64;
+std::once_flag g_lds_once[kMaxDevices][2];
+hipError_t g_lds_err[kMaxDevices][2];
+
+template <bool HALF>
+hipError_t ensure_lds_limit() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(g_lds_once[dev][HALF], [dev] {
+    g_lds_err[dev][HALF] = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  });
+  return g_lds_err[dev][HALF];
+}
+
+}  // namespace
+
+// Requires K % 128 == 0, 16-byte aligned weights, Mpad % 256 == 0 (qa/sa
+// padded with zero rows up to Mpad).
+hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
+  if (a.Mpad % kBM != 0) return hipErrorInvalidValue;
+  const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
+  hipError_t e;
+  if (a.half_w) {
+    if ((e = ensure_lds_limit<true>()) != hipSuccess) return e;
+    gemm_prefill256_kernel<true><<<tiles, 512, kLdsBytes, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M,
+                                                                    a.N, a.K, a.G, a.Mpad);
+  } else {
+    if ((e = ensure_lds_limit<false>()) != hipSuccess) return e;
+    gemm_prefill256_kernel<false><<<tiles, 512, kLdsBytes, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
+                                                                     a.M, a.N, a.K, a.G, a.Mpad);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace gk
