@@ -100,6 +100,29 @@ def time_loop(fn, iters, warmup):
     return time_graph(capture(fn, iters), iters)
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "block_fp8_gemm_bench.md")
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration), or None if not recorded."""
+    import re
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        m = re.match(r"traffic: kernel=(\S+) workload=(\S+) .* bytes=(\d+)", line)
+        if m and m.group(1) == kernel and m.group(2) == workload:
+            return int(m.group(3))
+    return None
+
+
+def kernel_short_name(name):
+    """Kernel name without its parameter list (and without the anonymous-namespace marker)."""
+    return name.replace("(anonymous namespace)::", "").split("(")[0]
+
+
 def rocprof_summary(directory):
     """Markdown tables from rocprofv3 csv output: kernel trace durations and PMC counters per dispatch shape.
 
@@ -119,7 +142,7 @@ def rocprof_summary(directory):
         agg = defaultdict(list)
         for r in csv.DictReader(open(path)):
             grid = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}x{r['Grid_Size_Z']}"
-            agg[(r["Kernel_Name"].split("(")[0], grid, r["Workgroup_Size_X"])].append(
+            agg[(kernel_short_name(r["Kernel_Name"]), grid, r["Workgroup_Size_X"])].append(
                 int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
         print(f"### kernel trace: {os.path.relpath(path, directory)}\n")
         print("| kernel | grid (threads) | wg | calls | avg us | median us | min us |")
@@ -131,7 +154,8 @@ def rocprof_summary(directory):
     for path in sorted(glob.glob(os.path.join(directory, "**", "*_counter_collection.csv"), recursive=True)):
         agg = defaultdict(list)
         for r in csv.DictReader(open(path)):
-            agg[(r["Kernel_Name"].split("(")[0], r["Grid_Size"], r["Counter_Name"])].append(float(r["Counter_Value"]))
+            agg[(kernel_short_name(r["Kernel_Name"]), r["Grid_Size"], r["Counter_Name"])].append(
+                float(r["Counter_Value"]))
         print(f"### counters: {os.path.relpath(path, directory)}\n")
         print("| kernel | grid (threads) | counter | dispatches | median | min | max |")
         print("|---|---|---|---|---|---|---|")
@@ -237,7 +261,9 @@ def main():
     b16 = gemm_bytes(16, n, k)
     achieved = b16 / (kernel_us_m16 * 1e-6) / 1e9
     result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                          "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                          "frac": round(achieved / PEAK_HBM_GBS, 4),
+                          "traffic": measured_traffic("gk::gemm_decode_kernel", "config2_M16"),
+                          "traffic_source": "profiles/block_fp8_gemm_bench.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
                           "kernel": "gk::gemm_decode_kernel (M=16, N=6144, K=4096)",
                           "bytes_per_launch": b16, "avg_launch_us": round(kernel_us_m16, 3)}
     result["decode_sweep"] = per_m
