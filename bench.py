@@ -1,6 +1,6 @@
 """Benchmark of the MI355X block-FP8 W8A8 GEMM (BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|mlp]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|mlp|moe]
 
 Workload (one "step"): the BASELINE configs[1] decode sweep -- one block-FP8
 GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
@@ -13,7 +13,8 @@ channels) and resident in HBM before timing starts.  Weight copies totalling
 value = algorithmic bytes of the sweep / time per sweep (GB/s), with bytes per
 GEMM B = N*K + 4*ceil(N/128)*ceil(K/128) + 2*M*K + 2*M*N.  Side measurements
 in the same JSON line: the prefill config (M=4096, N=K=7168; TFLOP/s against
-the dense FP8 MFMA peak), the MLP-pair decode config, the per-M sweep, the
+the dense FP8 MFMA peak), the MLP-pair decode config, the MoE layer (512
+tokens, 8 experts, top-2, H=4096, I=14336), the per-M sweep, the
 roofline of the dominant kernel (decode GEMM, HIP events on its stream) and
 the CPU oracle baseline timed on this host.
 """
@@ -170,7 +171,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["decode", "prefill", "mlp"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "mlp", "moe"], default=None)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print per-kernel, per-grid tables of a rocprofv3 csv output directory and exit")
     args = ap.parse_args()
@@ -307,6 +308,38 @@ def main():
                                    "gemm_kernel_TFLOPs": round(f / (ms4k * 1e-3) / 1e12, 1),
                                    "gemm_kernel_mfma_frac": round(f / (ms4k * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
         log(f"[bench] prefill: {result['prefill_m4096']}")
+
+    # ---- config 5: MoE layer ----------------------------------------------------------------------
+    if args.only in (None, "moe"):
+        t5, h5, i5, e5, k5 = 512, 4096, 14336, 8, 2
+        wg, sg, wdn, sdn = [], [], [], []
+        for i in range(e5):
+            a, b = synth.weight(2 * i5, h5, seed=5010 + i, device="cuda")
+            c, d = synth.weight(h5, i5, seed=6010 + i, device="cuda")
+            wg.append(a); sg.append(b); wdn.append(c); sdn.append(d)
+        wg, sg, wdn, sdn = torch.stack(wg), torch.stack(sg), torch.stack(wdn), torch.stack(sdn)
+        x5 = synth.activations(t5, h5, seed=5001).cuda()
+        lg5 = torch.randn(t5, e5, generator=torch.Generator().manual_seed(5002)).cuda()
+        o5 = torch.empty((t5, h5), dtype=torch.bfloat16, device="cuda")
+        ws5 = torch.empty(ops.moe_workspace_bytes(t5, h5, i5, e5, k5), dtype=torch.uint8, device="cuda")
+        ms5 = time_loop(lambda: ops.moe_block_fp8(x5, lg5, wg, sg, wdn, sdn, top_k=k5, out=o5, workspace=ws5),
+                        20, 3)
+        off = ops.moe_route(lg5, k5)[4].cpu()
+        rows_used = int(off[-1])
+        w_bytes = wg.numel() + wdn.numel() + 4 * (sg.numel() + sdn.numel())
+        io_bytes = 2 * t5 * h5 * 2 + 4 * t5 * e5
+        f_useful = 2 * t5 * k5 * (2 * i5 * h5 + h5 * i5)
+        f_padded = 2 * rows_used * (2 * i5 * h5 + h5 * i5)
+        result["moe_config5"] = {
+            "us": round(ms5 * 1e3, 1),
+            "weight_GBps": round((w_bytes + io_bytes) / (ms5 * 1e-3) / 1e9, 1),
+            "hbm_frac": round((w_bytes + io_bytes) / (ms5 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "TFLOPs": round(f_useful / (ms5 * 1e-3) / 1e12, 1),
+            "padded_TFLOPs": round(f_padded / (ms5 * 1e-3) / 1e12, 1),
+            "rows_used": rows_used, "rows_routed": t5 * k5, "weight_bytes": w_bytes}
+        log(f"[bench] moe: {result['moe_config5']}")
+        del wg, sg, wdn, sdn, ws5
+        torch.cuda.empty_cache()
 
     # ---- CPU baseline: the oracle on this host ----------------------------------------------------
     cpu = None

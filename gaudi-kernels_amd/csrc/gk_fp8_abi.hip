@@ -26,6 +26,8 @@ constexpr const char* kOps[] = {
     "gk_fp8_block_gemm_bf16_v1",    // quant -> MME -> reduce_bias.c / prefill chain, fused
     "gk_fp8_block_gemm_q_bf16_v1",  // GEMM on pre-quantized activations
     "gk_fp8_check_inputs_v1",       // block_fp8_oracle.py:22-24
+    "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
+    "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (build-defined)
 };
 constexpr uint32_t kNumOps = sizeof(kOps) / sizeof(kOps[0]);
 
@@ -335,6 +337,131 @@ gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, 
   st = read_status(workspace, &stat, s);
   if (st != GK_SUCCESS) return st;
   return stat.flags ? GK_NONFINITE_INPUT : GK_SUCCESS;
+}
+
+// ---- MoE ------------------------------------------------------------------------------
+namespace {
+
+struct MoeLayout {
+  int64_t rows;  // padded rows (multiple of 256)
+  size_t ids, wts, row_of, row_token, off, q1, sa1, hpre, q2, sa2, z, total;  // byte offsets
+};
+
+gk_status moe_rows(int64_t T, int64_t E, int top_k, int64_t* rows) {
+  if (T < 1 || E < 1 || E > gk::kMoeMaxExperts || top_k < 1 || top_k > 2 || top_k > E || T > (int64_t{1} << 24))
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  *rows = round_up(T * top_k + (gk::kMoeRowAlign - 1) * E, gk::kMoeRowAlign);
+  return GK_SUCCESS;
+}
+
+gk_status moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, MoeLayout* L) {
+  if (H < 128 || I < 128 || H % 128 || I % 128 || H > kMaxDim || I > kMaxDim / 2) return GK_INCOMPATIBLE_INPUT_SIZE;
+  gk_status st = moe_rows(T, E, top_k, &L->rows);
+  if (st != GK_SUCCESS) return st;
+  const size_t R = static_cast<size_t>(L->rows), tk = static_cast<size_t>(T * top_k);
+  size_t o = 0;
+  auto take = [&o](size_t bytes) { const size_t at = o; o += align256(bytes); return at; };
+  L->ids = take(tk * 4);
+  L->wts = take(tk * 4);
+  L->row_of = take(tk * 4);
+  L->row_token = take(R * 4);
+  L->off = take(static_cast<size_t>(E + 1) * 4);
+  L->q1 = take(R * static_cast<size_t>(H));
+  L->sa1 = take(R * static_cast<size_t>(H / 128) * 4);
+  L->hpre = take(R * static_cast<size_t>(2 * I) * 2);
+  L->q2 = take(R * static_cast<size_t>(I));
+  L->sa2 = take(R * static_cast<size_t>(I / 128) * 4);
+  L->z = take(R * static_cast<size_t>(H) * 2);
+  L->total = o;
+  return GK_SUCCESS;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+gk_status gk_fp8_moe_rows_max(int64_t T, int64_t E, int top_k, int64_t* rows_max) {
+  if (!rows_max) return GK_INVALID_ARGUMENT;
+  return moe_rows(T, E, top_k, rows_max);
+}
+
+gk_status gk_fp8_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, size_t* bytes) {
+  if (!bytes) return GK_INVALID_ARGUMENT;
+  MoeLayout L;
+  const gk_status st = moe_layout(T, H, I, E, top_k, &L);
+  if (st != GK_SUCCESS) return st;
+  *bytes = L.total;
+  return GK_SUCCESS;
+}
+
+gk_status gk_fp8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ld_logits, int top_k, int32_t* ids,
+                           float* wts, int32_t* row_of, int32_t* row_token, int64_t rows_max, int32_t* offsets,
+                           void* stream) {
+  if (!logits || !ids || !wts || !row_of || !row_token || !offsets) return GK_INVALID_ARGUMENT;
+  int64_t rows = 0;
+  gk_status st = moe_rows(T, E, top_k, &rows);
+  if (st != GK_SUCCESS) return st;
+  if (ld_logits < E) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (rows_max < rows) return GK_INSUFFICIENT_BUFFER;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  const gk::MoeRouting r{ids, wts, row_of, row_token, offsets};
+  return from_hip(gk::launch_moe_route(logits, static_cast<int>(T), static_cast<int>(E), ld_logits, top_k,
+                                       static_cast<int>(rows), r, static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, const float* logits, int64_t E,
+                          int64_t ld_logits, int top_k, const void* w_gu, const float* s_gu, int64_t I,
+                          const void* w_dn, const float* s_dn, void* y, int64_t ldy, uint32_t flags,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !logits || !w_gu || !s_gu || !w_dn || !s_dn || !y || !workspace) return GK_INVALID_ARGUMENT;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  MoeLayout L;
+  gk_status st = moe_layout(T, H, I, E, top_k, &L);
+  if (st != GK_SUCCESS) return st;
+  if (ldx < H || ld_logits < E) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldy < H) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (workspace_bytes < L.total) return GK_INSUFFICIENT_BUFFER;
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) || !aligned16(x) || !aligned16(y) || !aligned16(w_gu) ||
+      !aligned16(w_dn) || ldx % 8 || ldy % 8 || (reinterpret_cast<uintptr_t>(s_gu) & 3) ||
+      (reinterpret_cast<uintptr_t>(s_dn) & 3) || (reinterpret_cast<uintptr_t>(logits) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const bool half = (flags & GK_FLAG_NATIVE_HALF) != 0;
+  const int R = static_cast<int>(L.rows);
+  const gk::MoeRouting r{reinterpret_cast<int32_t*>(ws + L.ids), reinterpret_cast<float*>(ws + L.wts),
+                         reinterpret_cast<int32_t*>(ws + L.row_of), reinterpret_cast<int32_t*>(ws + L.row_token),
+                         reinterpret_cast<int32_t*>(ws + L.off)};
+  hipError_t e = gk::launch_moe_route(logits, static_cast<int>(T), static_cast<int>(E), ld_logits, top_k, R, r, s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  uint8_t* q1 = ws + L.q1;
+  float* sa1 = reinterpret_cast<float*>(ws + L.sa1);
+  e = gk::launch_act_quant_rows(static_cast<const uint16_t*>(x), ldx, static_cast<int>(H), r.row_token, R, q1, sa1,
+                                half, s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  uint16_t* hpre = reinterpret_cast<uint16_t*>(ws + L.hpre);
+  gk::GemmArgs a{};
+  a.qa = q1; a.sa = sa1; a.w = static_cast<const uint8_t*>(w_gu); a.sw = s_gu; a.bias = nullptr;
+  a.y = hpre; a.ldy = 2 * I; a.M = R; a.N = static_cast<int>(2 * I); a.K = static_cast<int>(H);
+  a.G = static_cast<int>(H / 128); a.Mpad = R; a.half_w = half;
+  e = gk::launch_gemm_grouped256(a, r.off, static_cast<int>(E), s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  uint8_t* q2 = ws + L.q2;
+  float* sa2 = reinterpret_cast<float*>(ws + L.sa2);
+  e = gk::launch_silu_mul_quant(hpre, 2 * I, static_cast<int>(I), r.off, static_cast<int>(E), R, q2, sa2, half, s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  uint16_t* z = reinterpret_cast<uint16_t*>(ws + L.z);
+  gk::GemmArgs d{};
+  d.qa = q2; d.sa = sa2; d.w = static_cast<const uint8_t*>(w_dn); d.sw = s_dn; d.bias = nullptr;
+  d.y = z; d.ldy = H; d.M = R; d.N = static_cast<int>(H); d.K = static_cast<int>(I);
+  d.G = static_cast<int>(I / 128); d.Mpad = R; d.half_w = half;
+  e = gk::launch_gemm_grouped256(d, r.off, static_cast<int>(E), s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  return from_hip(gk::launch_moe_combine(z, H, static_cast<int>(H), r.row_of, r.wts, static_cast<int>(T), top_k,
+                                         static_cast<uint16_t*>(y), ldy, s));
 }
 
 }  // extern "C"

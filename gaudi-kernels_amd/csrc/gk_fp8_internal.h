@@ -90,22 +90,29 @@ struct GemmArgs {
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);     // dispatches by M
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream);  // 256 x 256 tiles, Mpad % 256 == 0
+// Grouped (MoE) 256 x 256 GEMM over expert row segments; see gk_fp8_prefill.hip.
+hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, int n_groups, hipStream_t stream);
 hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream);
 
-// Grouped (MoE) variant: rows of qa are sorted by expert; expert e owns rows
-// [offsets[e], offsets[e+1]).  Weights/scales are stacked per expert.
-struct GroupedArgs {
-  const uint8_t* qa;
-  const float* sa;
-  const uint8_t* w;      // [E, N, K]
-  const float* sw;       // [E, NB, G]
-  const int32_t* offsets;  // [E + 1] device
-  uint16_t* y;           // [rows, N]
-  int rows, E, N, K, G;
-  int rows_pad;
-  int max_rows;          // host-known upper bound of rows of any expert
+// ---- MoE (gk_fp8_moe.hip) ------------------------------------------------------
+// Workspace pieces of one MoE layer call (device pointers).
+struct MoeRouting {
+  int32_t* ids;        // [T, k] expert of each slot
+  float* wts;          // [T, k] combine weight
+  int32_t* row_of;     // [T, k] padded row of each slot
+  int32_t* row_token;  // [rows_max] token of each padded row, -1 for padding
+  int32_t* off;        // [E + 1] padded expert starts (multiples of kMoeRowAlign)
 };
+constexpr int kMoeRowAlign = 256;
+constexpr int kMoeMaxExperts = 256;
 
-hipError_t launch_gemm_grouped(const GroupedArgs& a, hipStream_t stream);
+hipError_t launch_moe_route(const float* logits, int T, int E, int64_t ld_logits, int top_k, int rows_max,
+                            const MoeRouting& r, hipStream_t stream);
+hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_token, int rows,
+                                 uint8_t* q, float* sa, bool half, hipStream_t stream);
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off, int E, int rows,
+                                 uint8_t* q, float* sa, bool half, hipStream_t stream);
+hipError_t launch_moe_combine(const uint16_t* z, int64_t ldz, int H, const int32_t* row_of, const float* wts, int T,
+                              int top_k, uint16_t* y, int64_t ldy, hipStream_t stream);
 
 }  // namespace gk

@@ -81,6 +81,19 @@ __host__ __device__ inline float e4m3_value(uint32_t code) {
 }
 
 // fp32 -> bf16 bits, round to nearest even (NaN -> canonical quiet NaN).
+// Separately rounded fp32 multiply and add.  hipcc contracts a * b + c into
+// one fma by default (and __fmul_rn / __fadd_rn are plain operators in this
+// toolchain); operations emitted under contract(off) are never fused.
+__host__ __device__ inline float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
+__host__ __device__ inline float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 __host__ __device__ inline uint16_t bf16_rne(float v) {
   const uint32_t b = f32_bits(v);
   if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;

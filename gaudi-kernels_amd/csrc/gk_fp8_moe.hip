@@ -1,0 +1,253 @@
+// Block-FP8 MoE layer kernels for gfx950: routing, row gather + 1x128
+// quantization, fused SiLU-and-mul + quantization, weighted combine.  The
+// expert GEMMs are the grouped 256 x 256 kernel (gk_fp8_prefill.hip).
+//
+// The reference has no MoE code for this path; the layer follows BASELINE's
+// config 5 and is build-defined (the CPU restatement is oracle/moe.py):
+//   * route: top-k (k <= 2) experts by router logit, ties to the lower index;
+//     combine weights = softmax over the k selected logits (fp32);
+//   * rows: one row per (token, slot), ordered by expert then token; each
+//     expert's segment starts at a multiple of kMoeRowAlign (256) so a GEMM
+//     row tile never spans two experts; padding rows carry no token and are
+//     quantized as zeros;
+//   * act: h = bf16(silu(g) * u) in fp32 -- the reference's fused
+//     SiLU-and-mul (csrc/tpc/generic_dense/silu_and_mul_bf16.c:4-15), whose
+//     only rounding is the final product -- followed here by the same 1x128
+//     quantizer as the activations (block_fp8_oracle.py:25-28);
+//   * combine: y = bf16(w_0 z_0 + w_1 z_1) with each product and the sum
+//     rounded to fp32 (no fused multiply-add), slot order.
+
+#include "gk_fp8_internal.h"
+
+namespace gk {
+
+namespace {
+
+// ---- routing: one workgroup of 1024 threads ---------------------------------------
+// Phase 1: per token, the top-k experts (strictly greater wins; ties keep the
+// lower index) and softmax weights; an LDS histogram of expert counts.
+// Phase 2: padded segment starts.  Phase 3: for each expert, a block-wide
+// exclusive prefix count over tokens (in token order, 1024 at a time) gives
+// each slot's rank inside its expert -- stable, deterministic.
+constexpr int kRouteThreads = 1024;
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* __restrict__ logits, int T, int E,
+                                                                  int64_t ld, int top_k, int rows_max,
+                                                                  MoeRouting r) {
+  __shared__ int counts[kMoeMaxExperts];
+  __shared__ int offs[kMoeMaxExperts + 1];
+  __shared__ int carry[kMoeMaxExperts];
+  __shared__ int wave_sum[kRouteThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E; e += kRouteThreads) counts[e] = 0;
+  for (int i = tid; i < rows_max; i += kRouteThreads) r.row_token[i] = -1;
+  __syncthreads();
+
+  for (int t = tid; t < T; t += kRouteThreads) {
+    const float* row = logits + static_cast<int64_t>(t) * ld;
+    int best0 = 0;
+    float v0 = row[0];
+    for (int e = 1; e < E; ++e) {
+      const float v = row[e];
+      if (v > v0) { v0 = v; best0 = e; }
+    }
+    r.ids[t * top_k] = best0;
+    atomicAdd(&counts[best0], 1);
+    if (top_k == 2) {
+      int best1 = -1;
+      float v1 = 0.0f;
+      for (int e = 0; e < E; ++e) {
+        if (e == best0) continue;
+        const float v = row[e];
+        if (best1 < 0 || v > v1) { v1 = v; best1 = e; }
+      }
+      r.ids[t * 2 + 1] = best1;
+      atomicAdd(&counts[best1], 1);
+      // softmax over (v0, v1) with v0 >= v1: exp(0) = 1 and exp(v1 - v0), fp32
+      const float e1 = expf(v1 - v0);
+      const float s = 1.0f + e1;
+      r.wts[t * 2] = 1.0f / s;
+      r.wts[t * 2 + 1] = e1 / s;
+    } else {
+      r.wts[t] = 1.0f;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+      offs[e] = acc;
+      carry[e] = 0;
+      acc += (counts[e] + kMoeRowAlign - 1) / kMoeRowAlign * kMoeRowAlign;
+    }
+    offs[E] = acc;
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += kRouteThreads) r.off[e] = offs[e];
+
+  for (int base = 0; base < T; base += kRouteThreads) {
+    const int t = base + tid;
+    const bool live = t < T;
+    const int e0 = live ? r.ids[t * top_k] : -1;
+    const int e1 = (live && top_k == 2) ? r.ids[t * 2 + 1] : -1;
+    for (int e = 0; e < E; ++e) {
+      const int slot = (e0 == e) ? 0 : (e1 == e) ? 1 : -1;  // a token picks an expert at most once
+      const unsigned long long mask = __ballot(slot >= 0);
+      const int below = __popcll(mask & ((1ull << lane) - 1ull));
+      if (lane == 0) wave_sum[wave] = __popcll(mask);
+      __syncthreads();
+      int before = 0;
+      for (int v = 0; v < wave; ++v) before += wave_sum[v];
+      if (slot >= 0) {
+        const int row = offs[e] + carry[e] + before + below;
+        r.row_token[row] = t;
+        r.row_of[t * top_k + slot] = row;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int total = 0;
+        for (int v = 0; v < kRouteThreads / 64; ++v) total += wave_sum[v];
+        carry[e] += total;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---- gather + quantize rows: like act_quant_kernel, row r reads token row_token[r]
+template <bool HALF>
+__global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int K,
+                                                             int G, const int32_t* __restrict__ row_token,
+                                                             int rows, uint8_t* __restrict__ q,
+                                                             float* __restrict__ sa) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const int64_t total = static_cast<int64_t>(rows) * G;
+  const bool active = gid < total;
+  const int64_t row = active ? gid / G : 0;
+  const int g = active ? static_cast<int>(gid - row * G) : 0;
+  const int tok = active ? row_token[row] : -1;
+  const bool live = tok >= 0;
+  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
+  if (live) raw = *reinterpret_cast<const uint4*>(x + tok * ldx + g * 128 + sub * 8);
+  float s;
+  const uint2 codes = quant_group8(raw, live, HALF, &s);
+  if (active) {
+    const int64_t slot = static_cast<int64_t>(g) * rows + row;
+    *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = live ? codes : make_uint2(0u, 0u);
+    if (sub == 0) sa[slot] = live ? s : 0.0f;
+  }
+}
+
+// ---- fused SiLU-and-mul + 1x128 quantization ----------------------------------------
+// h: bf16 [rows, 2*inter] (gate | up), rows past off[E] are skipped.  Lane:
+// 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
+__device__ inline float silu_f32(float g) {
+  if (g <= -88.0f) return 0.0f;                 // silu_and_mul_bf16.c:10
+  if (!(fabsf(g) <= 3.4028235e38f)) return g;   // NaN / inf pass through (:11-12)
+  return g / (1.0f + expf(-g));
+}
+
+template <bool HALF>
+__global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ h, int64_t ldh, int inter,
+                                                             int G, const int32_t* __restrict__ off, int E,
+                                                             int rows, uint8_t* __restrict__ q,
+                                                             float* __restrict__ sa) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const int used = off[E];
+  const int64_t total = static_cast<int64_t>(used) * G;
+  if (gid >= total) return;  // a whole 16-lane group leaves together
+  const int64_t row = gid / G;
+  const int g = static_cast<int>(gid - row * G);
+  const uint16_t* hr = h + row * ldh + g * 128 + sub * 8;
+  const uint4 gv = *reinterpret_cast<const uint4*>(hr);
+  const uint4 uv = *reinterpret_cast<const uint4*>(hr + inter);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float g0 = bits_f32(gw[i] << 16), g1 = bits_f32(gw[i] & 0xffff0000u);
+    const float u0 = bits_f32(uw[i] << 16), u1 = bits_f32(uw[i] & 0xffff0000u);
+    const uint32_t p0 = bf16_rne(mul_rn(silu_f32(g0), u0));
+    const uint32_t p1 = bf16_rne(mul_rn(silu_f32(g1), u1));
+    out[i] = p0 | (p1 << 16);
+  }
+  float s;
+  const uint2 codes = quant_group8(make_uint4(out[0], out[1], out[2], out[3]), true, HALF, &s);
+  const int64_t slot = static_cast<int64_t>(g) * rows + row;
+  *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = codes;
+  if (sub == 0) sa[slot] = s;
+}
+
+// ---- combine: y[t] = bf16(w_0 z_0 + w_1 z_1), 8 columns per thread -------------------
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ z, int64_t ldz, int H,
+                                                          const int32_t* __restrict__ row_of,
+                                                          const float* __restrict__ wts, int T, int top_k,
+                                                          uint16_t* __restrict__ y, int64_t ldy) {
+  const int per_row = H / 8;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(T) * per_row) return;
+  const int t = static_cast<int>(i / per_row);
+  const int c = static_cast<int>(i - static_cast<int64_t>(t) * per_row) * 8;
+  float acc[8];
+  for (int k = 0; k < top_k; ++k) {
+    const float wk = wts[t * top_k + k];
+    const uint4 v = *reinterpret_cast<const uint4*>(z + static_cast<int64_t>(row_of[t * top_k + k]) * ldz + c);
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p0 = mul_rn(wk, bits_f32(w4[j] << 16));
+      const float p1 = mul_rn(wk, bits_f32(w4[j] & 0xffff0000u));
+      acc[2 * j] = k ? add_rn(acc[2 * j], p0) : p0;
+      acc[2 * j + 1] = k ? add_rn(acc[2 * j + 1], p1) : p1;
+    }
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = bf16_rne(acc[2 * j]) | (static_cast<uint32_t>(bf16_rne(acc[2 * j + 1])) << 16);
+  *reinterpret_cast<uint4*>(y + static_cast<int64_t>(t) * ldy + c) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+}  // namespace
+
+hipError_t launch_moe_route(const float* logits, int T, int E, int64_t ld_logits, int top_k, int rows_max,
+                            const MoeRouting& r, hipStream_t stream) {
+  if (E < 1 || E > kMoeMaxExperts || top_k < 1 || top_k > 2 || top_k > E) return hipErrorInvalidValue;
+  moe_route_kernel<<<1, kRouteThreads, 0, stream>>>(logits, T, E, ld_logits, top_k, rows_max, r);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_token, int rows,
+                                 uint8_t* q, float* sa, bool half, hipStream_t stream) {
+  const int G = K / 128;
+  const int64_t groups = static_cast<int64_t>(rows) * G;
+  const int blocks = static_cast<int>((groups + 15) / 16);
+  if (half)
+    act_quant_rows_kernel<true><<<blocks, 256, 0, stream>>>(x, ldx, K, G, row_token, rows, q, sa);
+  else
+    act_quant_rows_kernel<false><<<blocks, 256, 0, stream>>>(x, ldx, K, G, row_token, rows, q, sa);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off, int E, int rows,
+                                 uint8_t* q, float* sa, bool half, hipStream_t stream) {
+  const int G = inter / 128;
+  const int64_t groups = static_cast<int64_t>(rows) * G;
+  const int blocks = static_cast<int>((groups + 15) / 16);
+  if (half)
+    silu_mul_quant_kernel<true><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, E, rows, q, sa);
+  else
+    silu_mul_quant_kernel<false><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, E, rows, q, sa);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const uint16_t* z, int64_t ldz, int H, const int32_t* row_of, const float* wts, int T,
+                              int top_k, uint16_t* y, int64_t ldy, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(T) * (H / 8);
+  moe_combine_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(z, ldz, H, row_of, wts, T, top_k,
+                                                                                   y, ldy);
+  return hipGetLastError();
+}
+
+}  // namespace gk

@@ -60,20 +60,33 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
   for (int r = 0; r < 16; ++r) acc[r] = fmaf(t[r], f, acc[r]);
 }
 
-template <bool HALF>
+// Grouped (MoE) form: the rows of qa are expert segments starting at
+// group_off[e] (multiples of 256, group_off[n_groups] = rows in use); the
+// tile's rows belong to expert e, whose weights are w + e * w_stride and
+// scales sw + e * sw_stride.  Tiles past group_off[n_groups] exit at once.
+template <bool HALF, bool GROUPED>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
                                                               const float* __restrict__ sw,
                                                               const float* __restrict__ bias,
                                                               uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                              int K, int G, int Mpad) {
+                                                              int K, int G, int Mpad,
+                                                              const int32_t* __restrict__ group_off, int n_groups,
+                                                              int64_t w_stride, int64_t sw_stride) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 3, wm = wave >> 2;
   const int tiles_m = Mpad / kBM;
   const int tn = static_cast<int>(blockIdx.x) / tiles_m, tm = static_cast<int>(blockIdx.x) % tiles_m;
   const int n0 = tn * kBN, m0 = tm * kBM;  // consecutive workgroups share the weight panel
+  if (GROUPED) {
+    if (m0 >= group_off[n_groups]) return;  // uniform across the workgroup
+    int e = 0;
+    while (e + 1 < n_groups && group_off[e + 1] <= m0) ++e;
+    w += e * w_stride;
+    sw += e * sw_stride;
+  }
   const int64_t qstep = static_cast<int64_t>(Mpad) * 128;
 
   // Loader: wave w fills weight rows and activation rows [32 w, 32 w + 32) of
@@ -170,20 +183,35 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 
 // The 128 KB of dynamic LDS is above the default limit: raise it once per device.
 constexpr int kMaxDevices = 64;
-std::once_flag g_lds_once[kMaxDevices][2];
-hipError_t g_lds_err[kMaxDevices][2];
 
-template <bool HALF>
+std::once_flag g_lds_once[kMaxDevices][4];
+hipError_t g_lds_err[kMaxDevices][4];
+
+template <bool HALF, bool GROUPED>
 hipError_t ensure_lds_limit() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  std::call_once(g_lds_once[dev][HALF], [dev] {
-    g_lds_err[dev][HALF] = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0);
+  std::call_once(g_lds_once[dev][slot], [dev] {
+    g_lds_err[dev][slot] = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   });
-  return g_lds_err[dev][HALF];
+  return g_lds_err[dev][slot];
+}
+
+template <bool HALF, bool GROUPED>
+hipError_t launch256(const GemmArgs& a, const int32_t* group_off, int n_groups, int64_t w_stride,
+                     int64_t sw_stride, hipStream_t stream) {
+  hipError_t e = ensure_lds_limit<HALF, GROUPED>();
+  if (e != hipSuccess) return e;
+  const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
+  gemm_prefill256_kernel<HALF, GROUPED><<<tiles, 512, kLdsBytes, stream>>>(
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, n_groups, w_stride,
+      sw_stride);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -192,18 +220,18 @@ hipError_t ensure_lds_limit() {
 // padded with zero rows up to Mpad).
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
   if (a.Mpad % kBM != 0) return hipErrorInvalidValue;
-  const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
-  hipError_t e;
-  if (a.half_w) {
-    if ((e = ensure_lds_limit<true>()) != hipSuccess) return e;
-    gemm_prefill256_kernel<true><<<tiles, 512, kLdsBytes, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M,
-                                                                    a.N, a.K, a.G, a.Mpad);
-  } else {
-    if ((e = ensure_lds_limit<false>()) != hipSuccess) return e;
-    gemm_prefill256_kernel<false><<<tiles, 512, kLdsBytes, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
-                                                                     a.M, a.N, a.K, a.G, a.Mpad);
-  }
-  return hipGetLastError();
+  return a.half_w ? launch256<true, false>(a, nullptr, 0, 0, 0, stream)
+                  : launch256<false, false>(a, nullptr, 0, 0, 0, stream);
+}
+
+// Grouped form: a.Mpad = padded rows (multiple of 256), a.M = a.Mpad; weights
+// [n_groups][N][K], scales [n_groups][ceil(N/128)][G]; group_off on device.
+hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, int n_groups, hipStream_t stream) {
+  if (a.Mpad % kBM != 0 || n_groups < 1) return hipErrorInvalidValue;
+  const int64_t w_stride = static_cast<int64_t>(a.N) * a.K;
+  const int64_t sw_stride = static_cast<int64_t>((a.N + 127) / 128) * a.G;
+  return a.half_w ? launch256<true, true>(a, group_off, n_groups, w_stride, sw_stride, stream)
+                  : launch256<false, true>(a, group_off, n_groups, w_stride, sw_stride, stream);
 }
 
 }  // namespace gk

@@ -230,3 +230,80 @@ def inputs_finite(x, weight, scales):
         return False
     nat.check("gk_fp8_check_inputs", st)
     return True
+
+
+def moe_rows_max(tokens, n_experts, top_k=2):
+    """Padded row count of the expert-sorted layout (an upper bound of the rows in use)."""
+    rows = ctypes.c_int64(0)
+    nat.check("gk_fp8_moe_rows_max", nat.load().gk_fp8_moe_rows_max(tokens, n_experts, top_k, ctypes.byref(rows)))
+    return rows.value
+
+
+def moe_workspace_bytes(tokens, hidden, inter, n_experts, top_k=2):
+    nbytes = ctypes.c_size_t(0)
+    nat.check("gk_fp8_moe_workspace_bytes",
+              nat.load().gk_fp8_moe_workspace_bytes(tokens, hidden, inter, n_experts, top_k, ctypes.byref(nbytes)))
+    return nbytes.value
+
+
+def moe_route(logits, top_k=2):
+    """GPU routing -> (ids int32 [T, k], weights fp32 [T, k], row_of int32 [T, k], row_token int32 [R],
+    offsets int32 [E + 1]); R = moe_rows_max(T, E, k), rows past offsets[E] are unused (-1)."""
+    device = require_device(logits.device)
+    if logits.dtype != torch.float32 or logits.ndim != 2 or logits.stride(1) != 1:
+        raise ValueError("expected 2-D fp32 router logits [T, E] with unit column stride")
+    t, e = logits.shape
+    rows = moe_rows_max(t, e, top_k)
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=device)
+    wts = torch.empty((t, top_k), dtype=torch.float32, device=device)
+    row_of = torch.empty((t, top_k), dtype=torch.int32, device=device)
+    row_token = torch.empty(rows, dtype=torch.int32, device=device)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=device)
+    nat.check("gk_fp8_moe_route",
+              nat.load().gk_fp8_moe_route(_ptr(logits), t, e, logits.stride(0), top_k, _ptr(ids), _ptr(wts),
+                                          _ptr(row_of), _ptr(row_token), rows, _ptr(offsets), _stream(device)))
+    return ids, wts, row_of, row_token, offsets
+
+
+def moe_block_fp8(x, logits, w_gate_up, s_gate_up, w_down, s_down, *, top_k=2, native_half=False, out=None,
+                  workspace=None):
+    """Block-FP8 MoE layer: route, gather, gate_up GEMM, SiLU-and-mul, down GEMM, weighted combine.
+
+    x bf16 [T, H]; logits fp32 [T, E]; w_gate_up E4M3 [E, 2I, H] (gate rows first), s_gate_up fp32
+    [E, 2I/128, H/128]; w_down E4M3 [E, H, I], s_down fp32 [E, H/128, I/128] -> bf16 [T, H].
+    """
+    device = require_device(x.device)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("expected a 2-D bf16 activation with unit column stride")
+    if logits.dtype != torch.float32 or logits.ndim != 2 or logits.stride(1) != 1 or logits.shape[0] != x.shape[0]:
+        raise ValueError("expected fp32 router logits [T, E] with unit column stride")
+    t, h = x.shape
+    e = logits.shape[1]
+    for wt in (w_gate_up, w_down):
+        if wt.dtype not in (torch.float8_e4m3fn, torch.uint8) or wt.ndim != 3 or not wt.is_contiguous():
+            raise ValueError("expected contiguous E4M3 expert weights [E, N, K]")
+    inter = w_gate_up.shape[1] // 2
+    if w_gate_up.shape != (e, 2 * inter, h) or w_down.shape != (e, h, inter):
+        raise ValueError("expert weight shapes must be [E, 2I, H] and [E, H, I]")
+    if (s_gate_up.shape != (e, (2 * inter + 127) // 128, (h + 127) // 128)
+            or s_down.shape != (e, (h + 127) // 128, (inter + 127) // 128)):
+        raise ValueError("expert scale shapes must be [E, 2I/128, H/128] and [E, H/128, I/128]")
+    for tt in (logits, w_gate_up, s_gate_up, w_down, s_down):
+        if tt.device != device:
+            raise ValueError("all operands must be on the same GPU")
+    for st in (s_gate_up, s_down):
+        if st.dtype != torch.float32 or not st.is_contiguous():
+            raise ValueError("expected contiguous fp32 expert scales")
+    nbytes = moe_workspace_bytes(t, h, inter, e, top_k)
+    ws = _checked_workspace(workspace, nbytes, device)
+    if out is None:
+        out = torch.empty((t, h), dtype=torch.bfloat16, device=device)
+    elif out.dtype != torch.bfloat16 or out.shape != (t, h) or out.stride(1) != 1 or out.device != device:
+        raise ValueError("out must be bf16 [T, H] with unit column stride on the same GPU")
+    nat.check("gk_fp8_moe_bf16",
+              nat.load().gk_fp8_moe_bf16(_ptr(x), t, h, x.stride(0), _ptr(logits), e, logits.stride(0), top_k,
+                                         _ptr(_u8(w_gate_up)), _ptr(s_gate_up), inter, _ptr(_u8(w_down)),
+                                         _ptr(s_down), _ptr(out), out.stride(0),
+                                         nat.GK_FLAG_NATIVE_HALF if native_half else 0, _ptr(ws), ws.numel(),
+                                         _stream(device)))
+    return out

@@ -152,6 +152,49 @@ gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, 
                               const float* scales, int64_t n_scales, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* ---- block-FP8 MoE layer ------------------------------------
+ * No reference function: the reference has no MoE code for this path.  The
+ * layer is build-defined from the reference's pieces (oracle/moe.py restates
+ * it on the CPU): top-k (k = 1 or 2) experts per token by router logit, ties
+ * to the lower expert index, combine weights = softmax over the selected
+ * logits; rows grouped by expert in token order, each expert's segment padded
+ * to 256 rows; gate_up GEMM (block_fp8_oracle.py numerics) -> bf16 ->
+ * h = bf16(silu(gate) * up) (csrc/tpc/generic_dense/silu_and_mul_bf16.c) ->
+ * down GEMM -> y = bf16(sum_k w_k z_k).
+ *
+ * Shapes: x bf16 [T, H] (row stride ldx), logits fp32 [T, E] (row stride
+ * ld_logits), w_gu E4M3 [E, 2I, H] (gate rows 0..I-1, up rows I..2I-1) with
+ * scales fp32 [E, 2I/128, H/128], w_dn E4M3 [E, H, I] with scales fp32
+ * [E, H/128, I/128], y bf16 [T, H] (row stride ldy).  H and I multiples of
+ * 128, E <= 256; x, y, weights 16-byte aligned with ldx, ldy multiples of 8.
+ * flags: GK_FLAG_NATIVE_HALF only. */
+
+/* Padded row count of the expert-sorted layout: an upper bound of
+ * sum_e round_up(count_e, 256), i.e. round_up(T*top_k + 255*E, 256). */
+gk_status gk_fp8_moe_rows_max(int64_t T, int64_t E, int top_k, int64_t* rows_max);
+
+gk_status gk_fp8_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, size_t* bytes);
+
+/* Routing only: ids int32 [T, k], wts fp32 [T, k], row_of int32 [T, k]
+ * (padded row of each slot), row_token int32 [rows_max] (-1 = padding),
+ * offsets int32 [E + 1] (padded segment starts; offsets[E] = rows in use). */
+gk_status gk_fp8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ld_logits, int top_k, int32_t* ids,
+                           float* wts, int32_t* row_of, int32_t* row_token, int64_t rows_max, int32_t* offsets,
+                           void* stream);
+
+/* The whole layer, stream-ordered and asynchronous.  After the call the
+ * workspace holds the routing and the intermediates, in this order, each
+ * region starting at a 256-byte boundary (R = rows_max, G_H = H/128,
+ * G_I = I/128): ids, wts, row_of [T*k] x 4 B; row_token [R] int32;
+ * offsets [E+1] int32; gathered codes [G_H][R][128] u8 and scales [G_H][R]
+ * fp32; gate_up output bf16 [R][2I]; SiLU-and-mul codes [G_I][R][128] u8 and
+ * scales [G_I][R] fp32; down output bf16 [R][H].  Intermediate rows past
+ * offsets[E] are unspecified. */
+gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, const float* logits, int64_t E,
+                          int64_t ld_logits, int top_k, const void* w_gu, const float* s_gu, int64_t I,
+                          const void* w_dn, const float* s_dn, void* y, int64_t ldy, uint32_t flags,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,194 @@
+"""GPU block-FP8 MoE layer (gk_fp8_moe_route / gk_fp8_moe_bf16) against oracle/moe.py.
+
+Routing and the expert-sorted row layout are integer/index work: ids,
+row_token, row_of and offsets must be bit-exact; the two softmax weights are
+fp32 and within a few ulp (the device exp).  The layer output must meet the GEMM
+gate (max|y - ref| <= 1e-2 max|ref|, sum|y - ref| / sum|ref| <= 2e-3) at
+small sizes in full and at BASELINE config 5 (512 tokens, 8 experts, top-2,
+H=4096, I=14336) stage by stage on sampled tokens and end to end within the
+chain bound below, plus the size-independent property that
+permuting tokens permutes the output bit-for-bit (every row's arithmetic is
+independent of the other rows).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gaudi_kernels import ops
+from oracle import block_fp8, moe, synth
+
+pytestmark = pytest.mark.gpu
+
+# End-to-end bound for the two-GEMM chain at config 5.  The GEMM gate holds per
+# stage (test_moe_config5_stagewise_parity: each GEMM against the oracle fed
+# the device's own input, max 6e-3 / mean 5e-5 measured).  End to end, a one-ulp
+# bf16 difference in the gate_up output flips ~6% of the affected E4M3 codes of
+# the requantized intermediate (relative step 6-12%), and those flips sum over
+# K = 14336 in the down GEMM: measured max 2.2e-2 / mean 2.1e-3 on this input.
+CHAIN_MAX_REL = 4e-2
+CHAIN_MEAN_REL = 4e-3
+
+
+def check_routing(logits, top_k):
+    ids, wts, row_of, row_token, off = ops.moe_route(logits.cuda(), top_k)
+    torch.cuda.synchronize()
+    ids_ref, w_ref = moe.route(logits.numpy(), top_k)
+    rt_ref, _, ro_ref, off_ref, _ = moe.layout(ids_ref, logits.shape[1], 256)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_allclose(wts.cpu().numpy(), w_ref, rtol=5e-7, atol=0)
+    assert np.array_equal(off.cpu().numpy(), off_ref)
+    rt = row_token.cpu().numpy()
+    assert np.array_equal(rt[: len(rt_ref)], rt_ref)
+    assert np.all(rt[len(rt_ref):] == -1)
+    assert np.array_equal(row_of.cpu().numpy(), ro_ref)
+
+
+@pytest.mark.parametrize("t,e,k", [(512, 8, 2), (1, 8, 2), (37, 3, 1), (1000, 256, 2), (3000, 64, 2),
+                                   (2048, 2, 2), (5, 1, 1)])
+def test_routing_bit_exact(t, e, k):
+    gen = torch.Generator().manual_seed(t + e)
+    check_routing(torch.randn(t, e, generator=gen), k)
+
+
+def test_routing_ties_and_skew():
+    gen = torch.Generator().manual_seed(9)
+    lg = torch.randint(-2, 3, (700, 6), generator=gen).float()   # ties everywhere
+    check_routing(lg, 2)
+    lg = torch.randn(900, 16, generator=gen)
+    lg[:, 3] += 10.0                                              # every token picks expert 3
+    check_routing(lg, 2)
+
+
+def problem(t, h, inter, e, seed, device="cpu"):
+    x = synth.activations(t, h, seed)
+    gen = torch.Generator().manual_seed(seed + 1)
+    logits = torch.randn(t, e, generator=gen)
+    wg, sg, wd, sd = [], [], [], []
+    for i in range(e):
+        a, b = synth.weight(2 * inter, h, seed=seed + 10 + i, device=device)
+        c, d = synth.weight(h, inter, seed=seed + 1000 + i, device=device)
+        wg.append(a); sg.append(b); wd.append(c); sd.append(d)
+    return x, logits, torch.stack(wg), torch.stack(sg), torch.stack(wd), torch.stack(sd)
+
+
+def run(x, logits, wg, sg, wd, sd, **kw):
+    return ops.moe_block_fp8(x.cuda(), logits.cuda(), wg.cuda(), sg.cuda(), wd.cuda(), sd.cuda(), **kw)
+
+
+@pytest.mark.parametrize("t,h,inter,e,k", [(64, 256, 384, 4, 2), (200, 512, 256, 8, 2), (3, 384, 128, 8, 2),
+                                           (300, 256, 128, 3, 1), (1, 128, 128, 2, 2)])
+@pytest.mark.parametrize("native_half", [False, True])
+def test_moe_small_full_parity(t, h, inter, e, k, native_half):
+    x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=t + h + e)
+    y = run(x, logits, wg, sg, wd, sd, top_k=k, native_half=native_half).cpu()
+    ref = moe.moe_reference(x, logits, wg, sg, wd, sd, top_k=k, native_half=native_half)
+    max_rel, mean_rel = block_fp8.parity(y, ref)
+    assert max_rel <= block_fp8.MAX_REL_TOL and mean_rel <= block_fp8.MEAN_REL_TOL, (max_rel, mean_rel)
+
+
+def test_moe_strided_output_and_reuse():
+    x, logits, wg, sg, wd, sd = problem(96, 256, 256, 4, seed=77)
+    xs = torch.zeros(96, 384, dtype=torch.bfloat16)
+    xs[:, :256] = x
+    out = torch.full((96, 264), 7.0, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(ops.moe_workspace_bytes(96, 256, 256, 4, 2), dtype=torch.uint8, device="cuda")
+    ws.fill_(0xAB)  # stale workspace contents must not matter
+    y1 = run(xs[:, :256], logits, wg, sg, wd, sd, out=out[:, :256], workspace=ws)
+    y2 = run(x, logits, wg, sg, wd, sd, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.cpu(), y2.cpu())
+    assert torch.all(out[:, 256:].cpu() == 7.0)
+
+
+def regions(ws, t, h, inter, e, k):
+    """Views of the workspace regions documented for gk_fp8_moe_bf16 (include/gk_fp8.h)."""
+    rows = ops.moe_rows_max(t, e, k)
+    sizes = [("ids", t * k * 4), ("wts", t * k * 4), ("row_of", t * k * 4), ("row_token", rows * 4),
+             ("off", (e + 1) * 4), ("q1", rows * h), ("sa1", rows * h // 128 * 4), ("hpre", rows * 2 * inter * 2),
+             ("q2", rows * inter), ("sa2", rows * inter // 128 * 4), ("z", rows * h * 2)]
+    out, at = {}, 0
+    for name, nbytes in sizes:
+        out[name] = ws[at:at + nbytes]
+        at += (nbytes + 255) // 256 * 256
+    assert at == ops.moe_workspace_bytes(t, h, inter, e, k)
+    v = {n: out[n].view(torch.int32) for n in ("ids", "row_of", "row_token", "off")}
+    v["wts"] = out["wts"].view(torch.float32)
+    v["hpre"] = out["hpre"].view(torch.bfloat16).reshape(rows, 2 * inter)
+    v["z"] = out["z"].view(torch.bfloat16).reshape(rows, h)
+    v["q2"] = out["q2"].reshape(inter // 128, rows, 128)
+    v["sa2"] = out["sa2"].view(torch.float32).reshape(inter // 128, rows)
+    return {n: x.cpu() for n, x in v.items()}
+
+
+@pytest.mark.timeout(300)
+def test_moe_config5_stagewise_parity():
+    """Each stage of config 5 against the oracle, fed the device's own input to that stage.
+
+    gate_up and down: the GEMM gate per expert row set; SiLU-and-mul + quantization:
+    codes equal to the oracle's on the device's gate_up output except where the
+    device exp differs by an ulp; combine: bit-exact on the device's z and weights.
+    """
+    t, h, inter, e, k = 512, 4096, 14336, 8, 2
+    x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=5000, device="cuda")
+    ws = torch.empty(ops.moe_workspace_bytes(t, h, inter, e, k), dtype=torch.uint8, device="cuda")
+    y = ops.moe_block_fp8(x.cuda(), logits.cuda(), wg, sg, wd, sd, top_k=k, workspace=ws).cpu()
+    r = regions(ws, t, h, inter, e, k)
+    ids = r["ids"].reshape(t, k)
+    row_of = r["row_of"].reshape(t, k).long()
+    tokens = torch.randperm(t, generator=torch.Generator().manual_seed(2))[:12]
+    for x_e in range(e):
+        pairs = [(int(tok), s) for tok in tokens for s in range(k) if int(ids[tok, s]) == x_e]
+        if not pairs:
+            continue
+        rows = torch.tensor([int(row_of[tok, s]) for tok, s in pairs])
+        toks = torch.tensor([tok for tok, _ in pairs])
+        w_gu, s_gu, w_dn, s_dn = wg[x_e].cpu(), sg[x_e].cpu(), wd[x_e].cpu(), sd[x_e].cpu()
+        hpre = r["hpre"][rows]
+        ref_gu = block_fp8.reference(x[toks], w_gu, s_gu, row_chunk=16)
+        p_gu = block_fp8.parity(hpre, ref_gu)
+        hq = moe.silu_mul(hpre)
+        codes, sa = block_fp8.act_quant(hq)
+        got_codes = r["q2"][:, rows].permute(1, 0, 2).reshape(len(rows), -1)
+        mismatch = (got_codes != codes).float().mean().item()
+        got_sa = r["sa2"][:, rows].T
+        ref_dn = block_fp8.reference(hq, w_dn, s_dn, row_chunk=16)
+        p_dn = block_fp8.parity(r["z"][rows], ref_dn)
+        print(f"expert {x_e}: rows {len(rows)} gate_up {p_gu} code mismatch {mismatch:.2e} down {p_dn}", flush=True)
+        assert p_gu[0] <= block_fp8.MAX_REL_TOL and p_gu[1] <= block_fp8.MEAN_REL_TOL
+        assert mismatch <= 1e-3 and torch.allclose(got_sa, sa, rtol=1e-2, atol=0)
+        assert p_dn[0] <= block_fp8.MAX_REL_TOL and p_dn[1] <= block_fp8.MEAN_REL_TOL
+    # combine, bit-exact on the device's z and weights
+    wts = r["wts"].reshape(t, k)
+    z = r["z"].float()
+    acc = wts[:, 0:1] * z[row_of[:, 0]]
+    for s in range(1, k):
+        acc = acc + wts[:, s:s + 1] * z[row_of[:, s]]
+    assert torch.equal(y, acc.bfloat16())
+
+
+@pytest.mark.timeout(300)
+def test_moe_config5_sampled_parity_and_permutation():
+    t, h, inter, e = 512, 4096, 14336, 8
+    x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=5000, device="cuda")
+    xg, lg = x.cuda(), logits.cuda()
+    y = ops.moe_block_fp8(xg, lg, wg, sg, wd, sd, top_k=2)
+    perm = torch.randperm(t, generator=torch.Generator().manual_seed(1))
+    yp = ops.moe_block_fp8(xg[perm.cuda()].contiguous(), lg[perm.cuda()].contiguous(), wg, sg, wd, sd, top_k=2)
+    torch.cuda.synchronize()
+    assert torch.equal(yp.cpu(), y.cpu()[perm])
+    ids, _ = moe.route(logits.numpy(), 2)
+    counts = np.bincount(ids.reshape(-1), minlength=e)
+    assert counts.min() > 0 and counts.max() != counts.min()        # uneven, every expert used
+    tokens = torch.randperm(t, generator=torch.Generator().manual_seed(2))[:12].tolist()
+    ref = moe.moe_reference(x, logits, wg.cpu(), sg.cpu(), wd.cpu(), sd.cpu(), top_k=2, tokens=tokens)
+    max_rel, mean_rel = block_fp8.parity(y.cpu()[tokens], ref)
+    assert max_rel <= CHAIN_MAX_REL and mean_rel <= CHAIN_MEAN_REL, (max_rel, mean_rel)
+
+
+def test_moe_rejects_bad_shapes():
+    x, logits, wg, sg, wd, sd = problem(8, 256, 128, 2, seed=3)
+    with pytest.raises(ValueError):
+        run(x, logits, wg[:, :200], sg, wd, sd)
+    with pytest.raises(Exception):
+        run(x, logits, wg, sg, wd, sd, top_k=3)
