@@ -233,9 +233,10 @@ def main():
     kernel_us_m16 = None
     for m in ms_list:
         op_ms = time_loop(lambda: ops.block_fp8_gemm(xs[m], *rot.next(), out=outs[m], workspace=wss[m]), 100, 10)
-        _, m_pad, _ = ops.plan(m, n, k)
-        q, sa = ops.act_quant(xs[m], m_pad=m_pad)
-        kern_ms = time_loop(lambda: ops.block_fp8_gemm_q(q, sa, m, *rot.next(), out=outs[m]), 100, 10)
+        # the op's own activation layout for M <= 16: the decode fragment layout
+        q, sa = ops.act_quant(xs[m], decode_layout=True)
+        kern_ms = time_loop(lambda: ops.block_fp8_gemm_q(q, sa, m, *rot.next(), out=outs[m], decode_layout=True),
+                            100, 10)
         b = gemm_bytes(m, n, k)
         per_m[str(m)] = {"op_us": round(op_ms * 1e3, 2), "op_GBps": round(b / (op_ms * 1e-3) / 1e9, 1),
                          "gemm_kernel_us": round(kern_ms * 1e3, 2),

@@ -147,7 +147,7 @@ gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* sc
 
 gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, int64_t k, const void* w,
                    int64_t n, const float* scales, const float* bias, void* y, int64_t ldy, uint32_t flags,
-                   hipStream_t stream) {
+                   bool qpack, hipStream_t stream) {
   gk::GemmArgs a;
   a.qa = q;
   a.sa = sa;
@@ -163,6 +163,7 @@ gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, 
   a.Mpad = static_cast<int>(p.m_pad);
   a.half_w = (flags & GK_FLAG_NATIVE_HALF) != 0;
   a.dec = p.dec;
+  a.qpack = qpack;
   hipError_t e;
   switch (p.variant) {
     case GK_VARIANT_DECODE: e = gk::launch_gemm_decode(a, stream); break;
@@ -253,7 +254,9 @@ gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx
   if (!x || !q || !sa) return GK_INVALID_ARGUMENT;
   if (m < 1 || k < 1 || m > kMaxDim || k > kMaxDim || ldx < k) return GK_INCOMPATIBLE_INPUT_SIZE;
   if (m_pad < m || m_pad > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
-  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_DECODE_LAYOUT}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
+  if (packed && m_pad != gk::kDecodeMaxRows) return GK_INCOMPATIBLE_OUTPUT_SIZE;
   if ((reinterpret_cast<uintptr_t>(x) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
       (reinterpret_cast<uintptr_t>(sa) & 3))
     return GK_INCOMPATIBLE_DATA_TYPE;
@@ -261,7 +264,7 @@ gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx
   if (st != GK_SUCCESS) return st;
   return from_hip(gk::launch_act_quant(static_cast<const uint16_t*>(x), ldx, static_cast<int>(m),
                                        static_cast<int>(k), static_cast<int>(m_pad), static_cast<uint8_t*>(q), sa,
-                                       (flags & GK_FLAG_NATIVE_HALF) != 0, static_cast<hipStream_t>(stream)));
+                                       (flags & GK_FLAG_NATIVE_HALF) != 0, packed, static_cast<hipStream_t>(stream)));
 }
 
 gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, int* variant,
@@ -294,10 +297,13 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* q = static_cast<uint8_t*>(workspace);
   float* sa = reinterpret_cast<float*>(q + p.q_bytes);
+  // The decode variant takes its activations in the packed fragment layout.
+  const bool packed = p.variant == GK_VARIANT_DECODE;
   hipError_t e = gk::launch_act_quant(static_cast<const uint16_t*>(x), ldx, static_cast<int>(m), static_cast<int>(k),
-                                      static_cast<int>(p.m_pad), q, sa, (flags & GK_FLAG_NATIVE_HALF) != 0, s);
+                                      static_cast<int>(p.m_pad), q, sa, (flags & GK_FLAG_NATIVE_HALF) != 0, packed,
+                                      s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
-  return run_gemm(p, q, sa, m, k, w, n, scales, bias, y, ldy, flags, s);
+  return run_gemm(p, q, sa, m, k, w, n, scales, bias, y, ldy, flags, packed, s);
 }
 
 gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, int64_t m_pad, int64_t k,
@@ -305,9 +311,11 @@ gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, in
                                    int64_t scale_cols, const float* bias, void* y, int64_t ldy, uint32_t flags,
                                    void* stream) {
   if (!q || !sa) return GK_INVALID_ARGUMENT;
+  const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
   Plan p;
-  gk_status st = make_plan(m, n, k, flags, w, &p);
+  gk_status st = make_plan(m, n, k, flags & ~uint32_t{GK_FLAG_DECODE_LAYOUT}, w, &p);
   if (st != GK_SUCCESS) return st;
+  if (packed && p.variant != GK_VARIANT_DECODE) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
   if (m_pad != p.m_pad) return GK_INCOMPATIBLE_INPUT_SIZE;
   st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, y, ldy);
   if (st != GK_SUCCESS) return st;
@@ -315,7 +323,7 @@ gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, in
     return GK_INCOMPATIBLE_DATA_TYPE;
   st = current_device_ok();
   if (st != GK_SUCCESS) return st;
-  return run_gemm(p, static_cast<const uint8_t*>(q), sa, m, k, w, n, scales, bias, y, ldy, flags,
+  return run_gemm(p, static_cast<const uint8_t*>(q), sa, m, k, w, n, scales, bias, y, ldy, flags, packed,
                   static_cast<hipStream_t>(stream));
 }
 

@@ -142,8 +142,9 @@ __global__ __launch_bounds__(256) void codec_scales_kernel(const float* __restri
 // x: bf16 [M, K] with row stride ldx (elements).  Group-major outputs (the
 // reference quant op's {128, R, G} layout): q [G][Mpad][128] codes (rows >= M
 // and columns >= K are written as zero), sa [G][Mpad] fp32 (zero for rows >=
-// M).  One group = 16 lanes x 8 elements (quant_group8).
-template <bool HALF>
+// M).  One group = 16 lanes x 8 elements (quant_group8).  PACKED writes q in
+// the decode fragment layout instead (Mpad == 16; gk_fp8_internal.h).
+template <bool HALF, bool PACKED>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                         int K, int G, int Mpad, uint8_t* __restrict__ q,
                                                         float* __restrict__ sa, int vec_ok) {
@@ -168,7 +169,11 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   const uint2 codes = quant_group8(raw, live, HALF, &s);  // all 16 lanes of a group take part
   if (active) {
     const int64_t slot = static_cast<int64_t>(g) * Mpad + row;
-    *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = live ? codes : make_uint2(0u, 0u);
+    // bytes [8 sub, 8 sub + 8): 16-byte chunk c = sub / 2 goes to piece (c % 2, 16 (c / 2) + row)
+    const int64_t at = PACKED ? static_cast<int64_t>(g) * 2048 + ((sub >> 1) & 1) * 1024 +
+                                    (16 * (sub >> 2) + row) * 16 + (sub & 1) * 8
+                              : slot * 128 + sub * 8;
+    *reinterpret_cast<uint2*>(q + at) = live ? codes : make_uint2(0u, 0u);
     if (sub == 0) sa[slot] = live ? s : 0.0f;
   }
 }
@@ -212,15 +217,19 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
 }
 
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
-                            bool half, hipStream_t stream) {
+                            bool half, bool packed, hipStream_t stream) {
+  if (packed && Mpad != kDecodeMaxRows) return hipErrorInvalidValue;
   const int G = (K + 127) / 128;
   const int64_t groups = static_cast<int64_t>(Mpad) * G;
   const int blocks = static_cast<int>((groups + 15) / 16);  // 16 groups per 256-thread block
   const int vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (ldx % 8 == 0);
-  if (half)
-    act_quant_kernel<true><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok);
-  else
-    act_quant_kernel<false><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok);
+#define GK_AQ(H, P) act_quant_kernel<H, P><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok)
+  if (half) {
+    if (packed) GK_AQ(true, true); else GK_AQ(true, false);
+  } else {
+    if (packed) GK_AQ(false, true); else GK_AQ(false, false);
+  }
+#undef GK_AQ
   return hipGetLastError();
 }
 

@@ -32,17 +32,29 @@ namespace gk {
 // Decode variant (M <= 16): HBM-bound weight streaming.
 //
 // Workgroup = NW waves over R 16-row weight tiles (16R rows).  The waves split
-// the G groups into contiguous ranges.  Per group a wave loads the 16 x 128
-// activation fragment once (L2-resident, 2 x 16 bytes per lane) and the R
-// weight fragments (the four lanes of a row read 64 contiguous bytes per
-// instruction), then runs R MFMAs: activation traffic is 1/R of the weight
-// traffic.  U groups are loaded per batch so that U*R*2 16-byte weight loads
-// per lane are in flight.  The NW wave partials are summed in LDS in wave
-// order (deterministic) and rounded to bf16 with the bias.
+// the G groups into contiguous ranges; the NW partials are summed in LDS in
+// wave order (deterministic) and rounded to bf16 with the bias.
 //
-// Lane chunk pattern (A and B alike): lane (col, quad) holds bytes
-// [16 quad, 16 quad + 16) and [64 + 16 quad, 80 + 16 quad) of the group.
-template <int NW, int R, int U, bool HALF>
+// Weights are read fully coalesced: one load instruction covers 8 rows x 128
+// bytes of a group, lane l reading row 2 (l/16) + (l/8)%2, 16-byte chunk l%8,
+// so sixteen lanes read 256 contiguous bytes (the MFMA operand layout instead
+// puts 16 different rows in 16 consecutive lanes, which the memory pipeline
+// serves about 1.5-2x slower).  The tile goes through a wave-private 2 KB LDS
+// buffer -- chunk c of row r at slot c ^ ((r >> 1) & 7), bank-conflict free
+// for both the write and the fragment read -- into the MFMA layout.
+//
+// K permutation (A and B alike): lane (col, quad) holds bytes [32 quad,
+// 32 quad + 32) of the group.  Activations come in one of two layouts:
+//   * standard  qa [G][16][128]: lane reads token col at +32 quad, +32 quad+16;
+//   * packed    the decode fragment layout (launch_act_quant with packed):
+//     group g is 2 KB, piece (h, l) at g*2048 + h*1024 + 16 l holds bytes
+//     [32 (l/16) + 16 h, +16) of token l%16 -- the two loads of a wave read
+//     1 KB each, contiguous.
+// Tokens >= M read token M-1 (their results are never stored), so M < 16
+// touches fewer activation lines.  Every load is unconditional (indices are
+// clamped) and all loads of a step are issued before the first use: the
+// compiler then waits on them one by one instead of draining the queue.
+template <int NW, int R, int U, bool HALF, bool QPACK>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -51,49 +63,71 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
                                                               uint16_t* __restrict__ y, int64_t ldy, int M,
                                                               int N, int K, int G) {
   static_assert(16 * R <= 128 && NW >= R, "a workgroup's rows lie in one 128-row scale block");
+  __shared__ __attribute__((aligned(16))) uint8_t tile[NW][2048];
   __shared__ v4f red[NW][R][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int col = lane & 15, quad = lane >> 4;
   const int n0 = blockIdx.x * 16 * R;
+  const int lrow = 2 * (lane >> 4) + ((lane >> 3) & 1), lch = lane & 7;
   const uint8_t* wp[R];
+  int64_t d8[R];  // byte distance from row lrow to row lrow + 8 (rows past N re-read row N-1)
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    wp[r] = w + static_cast<int64_t>(min(n0 + 16 * r + col, N - 1)) * K + quad * 16;  // rows past N: dropped
-  const uint8_t* qp = qa + col * 128 + quad * 16;   // + g * 2048 (Mpad = 16)
-  const float* sap = sa + col;                      // + g * 16
+  for (int r = 0; r < R; ++r) {
+    const int a0 = min(n0 + 16 * r + lrow, N - 1), a1 = min(n0 + 16 * r + lrow + 8, N - 1);
+    wp[r] = w + static_cast<int64_t>(a0) * K + lch * 16;
+    d8[r] = static_cast<int64_t>(a1 - a0) * K;
+  }
+  const uint32_t woff0 = lrow * 128 + ((lch ^ ((lrow >> 1) & 7)) << 4);
+  const uint32_t woff1 = (lrow + 8) * 128 + ((lch ^ (((lrow + 8) >> 1) & 7)) << 4);
+  const uint32_t roff0 = col * 128 + (((2 * quad) ^ ((col >> 1) & 7)) << 4);
+  const uint32_t roff1 = col * 128 + (((2 * quad + 1) ^ ((col >> 1) & 7)) << 4);
+  const int tok = min(col, M - 1);
+  const uint8_t* qp = QPACK ? qa + (16 * quad + tok) * 16 : qa + tok * 128 + quad * 32;
+  constexpr int kQHi = QPACK ? 1024 : 16;
+  const float* sap = sa + tok;                      // + g * 16
   const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
+  uint8_t* buf = tile[wave];
 
   v4f acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   for (int g0 = gbeg; g0 < gend; g0 += U) {
     uint4 wa[U][R][2], qb[U][2];
-    float f[U];
+    float sv[U], wv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = min(g0 + u, gend - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        wa[u][r][0] = load_stream16(wp[r] + static_cast<int64_t>(g) * 128);
-        wa[u][r][1] = load_stream16(wp[r] + static_cast<int64_t>(g) * 128 + 64);
+        const uint8_t* p = wp[r] + static_cast<int64_t>(g) * 128;
+        wa[u][r][0] = load_stream16(p);
+        wa[u][r][1] = load_stream16(p + d8[r]);
       }
       const uint8_t* q = qp + static_cast<int64_t>(g) * 2048;
       qb[u][0] = *reinterpret_cast<const uint4*>(q);
-      qb[u][1] = *reinterpret_cast<const uint4*>(q + 64);
-      // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-      f[u] = (g0 + u < gend) ? sap[g * 16] * (HALF ? 2.0f * swp[g] : swp[g]) : 0.0f;
+      qb[u][1] = *reinterpret_cast<const uint4*>(q + kQHi);
+      sv[u] = sap[g * 16];
+      wv[u] = swp[g];
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the step is in flight before the first use
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const v8i b = pack8(qb[u][0], qb[u][1]);
+      // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
+      const float f = (g0 + u < gend) ? sv[u] * (HALF ? 2.0f * wv[u] : wv[u]) : 0.0f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const v4f t = mfma_f8(weight_frag<HALF>(wa[u][r][0], wa[u][r][1]), b);
-        acc[r][0] = fmaf(t[0], f[u], acc[r][0]);
-        acc[r][1] = fmaf(t[1], f[u], acc[r][1]);
-        acc[r][2] = fmaf(t[2], f[u], acc[r][2]);
-        acc[r][3] = fmaf(t[3], f[u], acc[r][3]);
+        *reinterpret_cast<uint4*>(buf + woff0) = wa[u][r][0];
+        *reinterpret_cast<uint4*>(buf + woff1) = wa[u][r][1];
+        const uint4 lo = *reinterpret_cast<const uint4*>(buf + roff0);
+        const uint4 hi = *reinterpret_cast<const uint4*>(buf + roff1);
+        const v4f t = mfma_f8(weight_frag<HALF>(lo, hi), b);
+        acc[r][0] = fmaf(t[0], f, acc[r][0]);
+        acc[r][1] = fmaf(t[1], f, acc[r][1]);
+        acc[r][2] = fmaf(t[2], f, acc[r][2]);
+        acc[r][3] = fmaf(t[3], f, acc[r][3]);
       }
     }
   }
@@ -260,40 +294,37 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __rest
 template <int NW, int R, int U>
 static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
-  if (a.half_w)
-    gemm_decode_kernel<NW, R, U, true><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
-                                                                      a.M, a.N, a.K, a.G);
-  else
-    gemm_decode_kernel<NW, R, U, false><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy,
-                                                                       a.M, a.N, a.K, a.G);
+#define GK_DECODE_LAUNCH(H, P)                                                                               \
+  gemm_decode_kernel<NW, R, U, H, P><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, \
+                                                                   a.M, a.N, a.K, a.G)
+  if (a.half_w) {
+    if (a.qpack) GK_DECODE_LAUNCH(true, true); else GK_DECODE_LAUNCH(true, false);
+  } else {
+    if (a.qpack) GK_DECODE_LAUNCH(false, true); else GK_DECODE_LAUNCH(false, false);
+  }
+#undef GK_DECODE_LAUNCH
   return hipGetLastError();
 }
 
 DecodeShape plan_decode_shape(int N, int G) {
-  // R: 16-row tiles per workgroup -- larger R cuts activation traffic (1/R of
-  // the weights) but leaves fewer workgroups; keep >= 192 of them for 256 CUs.
-  const int tiles = (N + 15) / 16;
-  const int r = tiles >= 4 * 384 ? 4 : tiles >= 2 * 192 ? 2 : 1;
-  const int wgs = (tiles + r - 1) / r;
-  // NW: waves per workgroup splitting K, for ~3072 waves in flight (12 per CU).
-  int nw = 4;
-  while (nw < 16 && wgs * nw * 2 <= 3072) nw *= 2;
+  // R: 16-row tiles per workgroup.  Activation fragments are loaded once per
+  // group for R weight tiles, so larger R cuts activation traffic, but the
+  // workgroup count (tiles / R) must stay near or above the 256 CUs.
+  // NW: waves splitting K; measured on MI355X (M = 16): N=6144/K=4096 best at
+  // (R, NW) = (2, 8), N=28672/K=4096 at (4, 4), N=4096/K=14336 at (1, 16).
   (void)G;
-  return DecodeShape{nw, r};
+  const int tiles = (N + 15) / 16;
+  if (tiles >= 1536) return DecodeShape{4, 4};
+  if (tiles >= 384) return DecodeShape{8, 2};
+  return DecodeShape{16, 1};
 }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
   const int key = a.dec.nw * 10 + a.dec.r;
   switch (key) {
-    case 41: return decode_launch<4, 1, 4>(a, stream);
-    case 42: return decode_launch<4, 2, 4>(a, stream);
     case 44: return decode_launch<4, 4, 4>(a, stream);
-    case 81: return decode_launch<8, 1, 4>(a, stream);
-    case 82: return decode_launch<8, 2, 4>(a, stream);
-    case 84: return decode_launch<8, 4, 2>(a, stream);
+    case 82: return decode_launch<8, 2, 2>(a, stream);
     case 161: return decode_launch<16, 1, 2>(a, stream);
-    case 162: return decode_launch<16, 2, 2>(a, stream);
-    case 164: return decode_launch<16, 4, 1>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }

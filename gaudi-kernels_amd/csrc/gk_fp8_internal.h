@@ -61,8 +61,11 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
                         float* scales_out, int64_t n_scales, uint32_t* flags, unsigned long long* rounded,
                         hipStream_t stream);
 
+// packed: the decode fragment layout (Mpad == 16): group g is 2 KB, the
+// 16-byte piece (h, l) at g*2048 + h*1024 + 16 l holds bytes
+// [32 (l/16) + 16 h, +16) of row l%16.  sa stays [G][Mpad].
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
-                            bool half, hipStream_t stream);
+                            bool half, bool packed, hipStream_t stream);
 
 // Decode variant shape: NW waves per workgroup (splitting K), R 16-row weight
 // tiles per workgroup.  Chosen by plan_decode_shape.
@@ -85,6 +88,7 @@ struct GemmArgs {
   int Mpad;           // 16 for the decode variant
   bool half_w;        // native_half: half-range codec on weight codes in-kernel, weight scales x2
   DecodeShape dec;    // decode variant only
+  bool qpack = false; // decode variant only: qa in the packed decode layout (launch_act_quant packed)
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);

@@ -42,6 +42,7 @@ GK_FLAG_NATIVE_HALF = 1
 GK_FLAG_FORCE_DECODE = 2
 GK_FLAG_FORCE_PREFILL = 4
 GK_FLAG_FORCE_GENERIC = 8
+GK_FLAG_DECODE_LAYOUT = 16
 
 GK_VARIANT_DECODE = 1
 GK_VARIANT_PREFILL = 2

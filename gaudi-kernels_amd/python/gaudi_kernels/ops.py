@@ -93,24 +93,34 @@ def _flags(native_half, variant):
     return flags
 
 
-def act_quant(x, *, native_half=False, m_pad=None):
+def act_quant(x, *, native_half=False, m_pad=None, decode_layout=False):
     """1x128 activation quantization on the GPU -> group-major (codes uint8 [G, m_pad, 128], sa fp32 [G, m_pad]).
 
     The layout of the reference's quant op output ({128, R, G} FCD-first, generic_fp8_glue.hpp:84-109).
+    decode_layout=True (m_pad 16) stores each group's 2 KB of codes in the decode fragment order
+    (include/gk_fp8.h, GK_FLAG_DECODE_LAYOUT) for block_fp8_gemm_q(..., decode_layout=True).
     """
     device = require_device(x.device)
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
         raise ValueError("expected a 2-D bf16 activation with unit column stride")
     m, k = x.shape
     g = (k + 127) // 128
-    m_pad = m if m_pad is None else m_pad
+    m_pad = (16 if decode_layout else m) if m_pad is None else m_pad
     q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
     sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
+    flags = (nat.GK_FLAG_NATIVE_HALF if native_half else 0) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
     lib = nat.load()
     nat.check("gk_fp8_act_quant_bf16",
-              lib.gk_fp8_act_quant_bf16(_ptr(x), m, k, x.stride(0), _ptr(q), _ptr(sa), m_pad,
-                                        nat.GK_FLAG_NATIVE_HALF if native_half else 0, _stream(device)))
+              lib.gk_fp8_act_quant_bf16(_ptr(x), m, k, x.stride(0), _ptr(q), _ptr(sa), m_pad, flags,
+                                        _stream(device)))
     return q, sa
+
+
+def decode_layout_to_standard(q):
+    """View helper: codes in the decode fragment layout [G, 16, 128] -> the standard [G, 16, 128] order."""
+    g = q.shape[0]
+    # piece (h, l) = bytes [32 (l // 16) + 16 h, +16) of row l % 16  ->  [G, h, quad, row, 16]
+    return q.reshape(g, 2, 4, 16, 16).permute(0, 3, 2, 1, 4).reshape(g, 16, 128)
 
 
 def _check_gemm_operands(weight, scales, bias, device):
@@ -164,12 +174,16 @@ def _checked_workspace(ws, nbytes, device):
     return ws
 
 
-def block_fp8_gemm_q(q, sa, m, weight, scales, bias=None, *, native_half=False, variant=None, out=None):
-    """GEMM on activations already quantized by act_quant(m_pad=plan(...)[1]) (group-major q, sa)."""
+def block_fp8_gemm_q(q, sa, m, weight, scales, bias=None, *, native_half=False, variant=None, out=None,
+                     decode_layout=False):
+    """GEMM on activations already quantized by act_quant(m_pad=plan(...)[1]) (group-major q, sa).
+
+    decode_layout: q comes from act_quant(..., decode_layout=True); the plan must be the decode variant.
+    """
     device = require_device(q.device)
     _check_gemm_operands(weight, scales, bias, device)
     n, k = weight.shape
-    flags = _flags(native_half, variant)
+    flags = _flags(native_half, variant) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
     w8 = _u8(weight)
     g = (k + 127) // 128
     if q.shape != (g, q.shape[1], 128) or sa.shape != (g, q.shape[1]) or not (q.is_contiguous() and sa.is_contiguous()):

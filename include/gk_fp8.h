@@ -59,6 +59,7 @@ typedef enum gk_status {
 #define GK_FLAG_FORCE_DECODE 2u    /* force the M <= 16 weight-streaming variant (requires M <= 16) */
 #define GK_FLAG_FORCE_PREFILL 4u   /* force the LDS-tiled MFMA variant */
 #define GK_FLAG_FORCE_GENERIC 8u   /* force the any-shape variant */
+#define GK_FLAG_DECODE_LAYOUT 16u  /* act_quant / q GEMM only: quantized activations in the decode fragment layout */
 
 /* Variants reported by gk_fp8_block_gemm_plan. */
 #define GK_VARIANT_DECODE 1
@@ -109,7 +110,12 @@ gk_status gk_fp8_codec_half_to_ocp(const void* src, void* dst, int64_t n, const 
  * gk_fp8_block_quant_bf16_v1 op (activation_native.c:9-30, glue
  * generic_fp8_glue.hpp:84-109) in that op's group-major layout ({128, R, G}
  * FCD-first): q codes [G][m_pad][128] (G = ceil(k/128)), sa fp32 [G][m_pad];
- * rows >= m and columns >= k are written as zero.  m_pad >= m. */
+ * rows >= m and columns >= k are written as zero.  m_pad >= m.
+ * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_DECODE_LAYOUT (m_pad must be 16) writes
+ * q in the decode fragment layout the M <= 16 GEMM reads with coalesced
+ * loads: group g is 2 KB and the 16-byte piece (h, l), h < 2, l < 64, at
+ * g*2048 + h*1024 + 16 l holds bytes [32 (l/16) + 16 h, +16) of row l%16.
+ * sa keeps its [G][16] layout. */
 gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, void* q, float* sa,
                                 int64_t m_pad, uint32_t flags, void* stream);
 
@@ -137,7 +143,8 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
 
 /* The same GEMM on activations already quantized by gk_fp8_act_quant_bf16
  * (q [G][m_pad][128], sa [G][m_pad]); m_pad must equal the plan's m_pad for
- * these flags.  No workspace.  (The second half of the Gaudi2 decode chain:
+ * these flags.  GK_FLAG_DECODE_LAYOUT: q is in the decode fragment layout
+ * (the plan must be the decode variant).  No workspace.  (The second half of the Gaudi2 decode chain:
  * MME partials + reduce_bias.c, fused.) */
 gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, int64_t m_pad, int64_t k,
                                    const void* w, int64_t n, const float* scales, int64_t scale_rows,

@@ -154,6 +154,15 @@ def test_q_entry_point_matches_fused():
         y1 = ops.block_fp8_gemm_q(q, sa, m, w.cuda(), s.cuda(), variant=variant)  # decode: pre-quantized path
         y2 = ops.block_fp8_gemm(x, w.cuda(), s.cuda(), variant=variant)
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    # decode fragment layout (what the fused op uses internally), both weight modes
+    for native_half in (False, True):
+        q, sa = ops.act_quant(x, native_half=native_half, decode_layout=True)
+        y1 = ops.block_fp8_gemm_q(q, sa, m, w.cuda(), s.cuda(), native_half=native_half, decode_layout=True)
+        y2 = ops.block_fp8_gemm(x, w.cuda(), s.cuda(), native_half=native_half)
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    with pytest.raises(Exception):
+        q, sa = ops.act_quant(x, decode_layout=True)
+        ops.block_fp8_gemm_q(q, sa, m, w.cuda(), s.cuda(), variant="prefill", decode_layout=True)
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 6144, 4096), (5, 4096, 14336), (1, 200, 1024), (16, 64, 128),
