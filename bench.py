@@ -104,9 +104,10 @@ def time_loop(fn, iters, warmup):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "block_fp8_gemm_bench.md")
 
 
-def measured_traffic(kernel, workload):
-    """HBM bytes per launch of `kernel` on `workload` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration), or None if not recorded."""
+def measured_traffic(kernel_prefix, workload):
+    """HBM bytes per launch of the kernel whose name starts with `kernel_prefix` on `workload`, from the
+    committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration),
+    or None if not recorded."""
     import re
     try:
         text = open(TRAFFIC_PROFILE).read()
@@ -114,7 +115,7 @@ def measured_traffic(kernel, workload):
         return None
     for line in text.splitlines():
         m = re.match(r"traffic: kernel=(\S+) workload=(\S+) .* bytes=(\d+)", line)
-        if m and m.group(1) == kernel and m.group(2) == workload:
+        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload:
             return int(m.group(3))
     return None
 
@@ -152,6 +153,7 @@ def rocprof_summary(directory):
             print(f"| `{name}` | {grid} | {wg} | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {med(v) / 1e3:.2f} | "
                   f"{min(v) / 1e3:.2f} |")
         print()
+    counters = defaultdict(list)
     for path in sorted(glob.glob(os.path.join(directory, "**", "*_counter_collection.csv"), recursive=True)):
         agg = defaultdict(list)
         for r in csv.DictReader(open(path)):
@@ -162,7 +164,29 @@ def rocprof_summary(directory):
         print("|---|---|---|---|---|---|---|")
         for (name, grid, ctr), v in sorted(agg.items()):
             print(f"| `{name}` | {grid} | {ctr} | {len(v)} | {med(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
+            counters[(name, grid, ctr)] += v
         print()
+    # Traffic: the 256 MiB copy of bench.py (largest __amd_rocclr_copyBuffer dispatch) calibrates the
+    # counters; each gk decode GEMM dispatch shape of a `--only decode` run (config 2) gets a line.
+    copy = {}
+    for (n, g, c), v in counters.items():
+        if n == "__amd_rocclr_copyBuffer":
+            copy[c] = max(copy.get(c, 0.0), max(v))
+    copy_bytes = 256 << 20
+    if "FETCH_SIZE" in copy and "WRITE_SIZE" in copy:
+        fs, ws = copy_bytes / 1024 / copy["FETCH_SIZE"], copy_bytes / 1024 / copy["WRITE_SIZE"]
+        print(f"copy calibration: FETCH_SIZE {copy['FETCH_SIZE']:.1f} KiB and WRITE_SIZE {copy['WRITE_SIZE']:.1f} KiB "
+              f"for {copy_bytes} bytes each way: scales {fs:.4f} / {ws:.4f}\n")
+        for (name, grid, ctr), v in sorted(counters.items()):
+            if ctr != "FETCH_SIZE" or not name.replace("void ", "").startswith("gk::gemm_decode_kernel"):
+                continue
+            wv = counters.get((name, grid, "WRITE_SIZE"))
+            if not wv:
+                continue
+            f_kib, w_kib = med(v), med(wv)
+            total = int(round(f_kib * 1024 * fs + w_kib * 1024 * ws))
+            print(f"traffic: kernel={name.replace('void ', '').replace(' ', '')} workload=config2 grid={grid} fetch_kib={f_kib:.1f} "
+                  f"write_kib={w_kib:.1f} fetch_scale={fs:.4f} write_scale={ws:.4f} bytes={total}\n")
 
 
 def main():
@@ -264,7 +288,7 @@ def main():
     achieved = b16 / (kernel_us_m16 * 1e-6) / 1e9
     result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(achieved / PEAK_HBM_GBS, 4),
-                          "traffic": measured_traffic("gk::gemm_decode_kernel", "config2_M16"),
+                          "traffic": measured_traffic("gk::gemm_decode_kernel", "config2"),
                           "traffic_source": "profiles/block_fp8_gemm_bench.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
                           "kernel": "gk::gemm_decode_kernel (M=16, N=6144, K=4096)",
                           "bytes_per_launch": b16, "avg_launch_us": round(kernel_us_m16, 3)}
