@@ -352,7 +352,8 @@ namespace {
 
 struct MoeLayout {
   int64_t rows;  // padded rows (multiple of 256)
-  size_t ids, wts, row_of, row_token, off, q1, sa1, hpre, q2, sa2, z, total;  // byte offsets
+  int kparts;    // K split of the down GEMM (fp32 partial planes of z)
+  size_t ids, wts, row_of, row_token, off, cnt, q1, sa1, hpre, q2, sa2, z, total;  // byte offsets
 };
 
 gk_status moe_rows(int64_t T, int64_t E, int top_k, int64_t* rows) {
@@ -366,6 +367,8 @@ gk_status moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, MoeL
   if (H < 128 || I < 128 || H % 128 || I % 128 || H > kMaxDim || I > kMaxDim / 2) return GK_INCOMPATIBLE_INPUT_SIZE;
   gk_status st = moe_rows(T, E, top_k, &L->rows);
   if (st != GK_SUCCESS) return st;
+  // the grouped GEMMs address the gathered activations with 32-bit offsets
+  if (L->rows * (H > I ? H : I) > int64_t{0xffffffff}) return GK_INCOMPATIBLE_INPUT_SIZE;
   const size_t R = static_cast<size_t>(L->rows), tk = static_cast<size_t>(T * top_k);
   size_t o = 0;
   auto take = [&o](size_t bytes) { const size_t at = o; o += align256(bytes); return at; };
@@ -374,12 +377,16 @@ gk_status moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, MoeL
   L->row_of = take(tk * 4);
   L->row_token = take(R * 4);
   L->off = take(static_cast<size_t>(E + 1) * 4);
+  L->cnt = take(static_cast<size_t>(E) * 4);
   L->q1 = take(R * static_cast<size_t>(H));
   L->sa1 = take(R * static_cast<size_t>(H / 128) * 4);
   L->hpre = take(R * static_cast<size_t>(2 * I) * 2);
   L->q2 = take(R * static_cast<size_t>(I));
   L->sa2 = take(R * static_cast<size_t>(I / 128) * 4);
-  L->z = take(R * static_cast<size_t>(H) * 2);
+  // The down GEMM has (rows / 256) * ceil(H / 256) workgroups at most: below two
+  // per CU it splits K in two halves (fp32 partial planes summed by the combine).
+  L->kparts = (L->rows / 256) * ((H + 255) / 256) < 512 ? 2 : 1;
+  L->z = take(static_cast<size_t>(L->kparts) * R * static_cast<size_t>(H) * 4);
   L->total = o;
   return GK_SUCCESS;
 }
@@ -413,7 +420,7 @@ gk_status gk_fp8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ld
   if (rows_max < rows) return GK_INSUFFICIENT_BUFFER;
   st = current_device_ok();
   if (st != GK_SUCCESS) return st;
-  const gk::MoeRouting r{ids, wts, row_of, row_token, offsets};
+  const gk::MoeRouting r{ids, wts, row_of, row_token, offsets, nullptr};
   return from_hip(gk::launch_moe_route(logits, static_cast<int>(T), static_cast<int>(E), ld_logits, top_k,
                                        static_cast<int>(rows), r, static_cast<hipStream_t>(stream)));
 }
@@ -442,7 +449,7 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   const int R = static_cast<int>(L.rows);
   const gk::MoeRouting r{reinterpret_cast<int32_t*>(ws + L.ids), reinterpret_cast<float*>(ws + L.wts),
                          reinterpret_cast<int32_t*>(ws + L.row_of), reinterpret_cast<int32_t*>(ws + L.row_token),
-                         reinterpret_cast<int32_t*>(ws + L.off)};
+                         reinterpret_cast<int32_t*>(ws + L.off), reinterpret_cast<int32_t*>(ws + L.cnt)};
   hipError_t e = gk::launch_moe_route(logits, static_cast<int>(T), static_cast<int>(E), ld_logits, top_k, R, r, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   uint8_t* q1 = ws + L.q1;
@@ -455,20 +462,22 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   a.qa = q1; a.sa = sa1; a.w = static_cast<const uint8_t*>(w_gu); a.sw = s_gu; a.bias = nullptr;
   a.y = hpre; a.ldy = 2 * I; a.M = R; a.N = static_cast<int>(2 * I); a.K = static_cast<int>(H);
   a.G = static_cast<int>(H / 128); a.Mpad = R; a.half_w = half;
-  e = gk::launch_gemm_grouped256(a, r.off, static_cast<int>(E), s);
+  e = gk::launch_gemm_grouped256(a, r.off, r.cnt, static_cast<int>(E), 1, nullptr, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   uint8_t* q2 = ws + L.q2;
   float* sa2 = reinterpret_cast<float*>(ws + L.sa2);
-  e = gk::launch_silu_mul_quant(hpre, 2 * I, static_cast<int>(I), r.off, static_cast<int>(E), R, q2, sa2, half, s);
+  e = gk::launch_silu_mul_quant(hpre, 2 * I, static_cast<int>(I), r.off, r.row_token, static_cast<int>(E), R, q2, sa2,
+                                half, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
-  uint16_t* z = reinterpret_cast<uint16_t*>(ws + L.z);
+  float* z = reinterpret_cast<float*>(ws + L.z);
   gk::GemmArgs d{};
   d.qa = q2; d.sa = sa2; d.w = static_cast<const uint8_t*>(w_dn); d.sw = s_dn; d.bias = nullptr;
-  d.y = z; d.ldy = H; d.M = R; d.N = static_cast<int>(H); d.K = static_cast<int>(I);
+  d.y = nullptr; d.ldy = H; d.M = R; d.N = static_cast<int>(H); d.K = static_cast<int>(I);
   d.G = static_cast<int>(I / 128); d.Mpad = R; d.half_w = half;
-  e = gk::launch_gemm_grouped256(d, r.off, static_cast<int>(E), s);
+  e = gk::launch_gemm_grouped256(d, r.off, r.cnt, static_cast<int>(E), L.kparts, z, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
-  return from_hip(gk::launch_moe_combine(z, H, static_cast<int>(H), r.row_of, r.wts, static_cast<int>(T), top_k,
+  return from_hip(gk::launch_moe_combine(z, L.kparts, static_cast<int64_t>(R) * H, static_cast<int>(H), r.row_of,
+                                         r.wts, static_cast<int>(T), top_k,
                                          static_cast<uint16_t*>(y), ldy, s));
 }
 

@@ -331,7 +331,8 @@ hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
 
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
   // M > 128: 256 x 256 tiles (gk_fp8_prefill.hip); smaller M wastes less on 128 x 128 tiles.
-  if (a.M > 128) return launch_gemm_prefill256(a, stream);
+  // The 256 kernel addresses each operand panel with 32-bit offsets.
+  if (a.M > 128 && prefill256_fits(a)) return launch_gemm_prefill256(a, stream);
   const dim3 grid((a.N + kPB - 1) / kPB, (a.M + kPB - 1) / kPB);
   if (a.half_w)
     gemm_prefill_kernel<true><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,

@@ -94,8 +94,20 @@ struct GemmArgs {
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream);     // dispatches by M
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream);  // 256 x 256 tiles, Mpad % 256 == 0
+// The 256 x 256 kernels address a 256-row weight panel and the whole
+// group-major activation array with 32-bit byte offsets.
+inline bool prefill256_fits(const GemmArgs& a) {
+  return static_cast<int64_t>(a.Mpad) * a.G * 128 <= int64_t{0xffffffff} &&
+         static_cast<int64_t>(256) * a.K <= int64_t{0xffffffff};
+}
 // Grouped (MoE) 256 x 256 GEMM over expert row segments; see gk_fp8_prefill.hip.
-hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, int n_groups, hipStream_t stream);
+// Grouped (MoE) 256 x 256 GEMM over expert row segments (gk_fp8_prefill.hip):
+// segment e starts at group_off[e] (multiple of 256) and holds group_cnt[e]
+// live rows; 32-row blocks past the live rows are skipped.  yp == nullptr:
+// bf16 y; otherwise fp32 planes yp[part][M][N] (a.y unused), one per K part
+// (kparts = 1 or 2; 2 splits the groups in halves).
+hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt,
+                                  int n_groups, int kparts, float* yp, hipStream_t stream);
 hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream);
 
 // ---- MoE (gk_fp8_moe.hip) ------------------------------------------------------
@@ -106,6 +118,7 @@ struct MoeRouting {
   int32_t* row_of;     // [T, k] padded row of each slot
   int32_t* row_token;  // [rows_max] token of each padded row, -1 for padding
   int32_t* off;        // [E + 1] padded expert starts (multiples of kMoeRowAlign)
+  int32_t* cnt;        // [E] live rows of each expert
 };
 constexpr int kMoeRowAlign = 256;
 constexpr int kMoeMaxExperts = 256;
@@ -114,9 +127,11 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int64_t ld_logits
                             const MoeRouting& r, hipStream_t stream);
 hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_token, int rows,
                                  uint8_t* q, float* sa, bool half, hipStream_t stream);
-hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off, int E, int rows,
-                                 uint8_t* q, float* sa, bool half, hipStream_t stream);
-hipError_t launch_moe_combine(const uint16_t* z, int64_t ldz, int H, const int32_t* row_of, const float* wts, int T,
-                              int top_k, uint16_t* y, int64_t ldy, hipStream_t stream);
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off,
+                                 const int32_t* row_token, int E, int rows, uint8_t* q, float* sa, bool half,
+                                 hipStream_t stream);
+// z: kparts fp32 planes [kparts][rows][H] of the down GEMM; y[t] = bf16(sum_k w_k bf16(sum_p z_p[row])).
+hipError_t launch_moe_combine(const float* z, int kparts, int64_t plane, int H, const int32_t* row_of,
+                              const float* wts, int T, int top_k, uint16_t* y, int64_t ldy, hipStream_t stream);
 
 }  // namespace gk

@@ -84,6 +84,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
   }
   __syncthreads();
   for (int e = tid; e <= E; e += kRouteThreads) r.off[e] = offs[e];
+  if (r.cnt)
+    for (int e = tid; e < E; e += kRouteThreads) r.cnt[e] = counts[e];
 
   for (int base = 0; base < T; base += kRouteThreads) {
     const int t = base + tid;
@@ -140,8 +142,9 @@ __global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __r
 }
 
 // ---- fused SiLU-and-mul + 1x128 quantization ----------------------------------------
-// h: bf16 [rows, 2*inter] (gate | up), rows past off[E] are skipped.  Lane:
-// 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
+// h: bf16 [rows, 2*inter] (gate | up); rows past off[E] and padding rows
+// (row_token < 0, whose gate_up outputs were never computed) are skipped.
+// Lane: 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
 __device__ inline float silu_f32(float g) {
   if (g <= -88.0f) return 0.0f;                 // silu_and_mul_bf16.c:10
   if (!(fabsf(g) <= 3.4028235e38f)) return g;   // NaN / inf pass through (:11-12)
@@ -150,7 +153,8 @@ __device__ inline float silu_f32(float g) {
 
 template <bool HALF>
 __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ h, int64_t ldh, int inter,
-                                                             int G, const int32_t* __restrict__ off, int E,
+                                                             int G, const int32_t* __restrict__ off,
+                                                             const int32_t* __restrict__ row_token, int E,
                                                              int rows, uint8_t* __restrict__ q,
                                                              float* __restrict__ sa) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
@@ -159,6 +163,7 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __r
   const int64_t total = static_cast<int64_t>(used) * G;
   if (gid >= total) return;  // a whole 16-lane group leaves together
   const int64_t row = gid / G;
+  if (row_token[row] < 0) return;  // padding row: a whole 16-lane group leaves together
   const int g = static_cast<int>(gid - row * G);
   const uint16_t* hr = h + row * ldh + g * 128 + sub * 8;
   const uint4 gv = *reinterpret_cast<const uint4*>(hr);
@@ -181,8 +186,10 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __r
 }
 
 // ---- combine: y[t] = bf16(w_0 z_0 + w_1 z_1), 8 columns per thread -------------------
-__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ z, int64_t ldz, int H,
-                                                          const int32_t* __restrict__ row_of,
+// z_k = bf16(sum_p zp[p][row_of[t, k]]): the down GEMM's output rounded to bf16
+// once, from its kparts fp32 partial planes.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ z, int kparts, int64_t plane,
+                                                          int H, const int32_t* __restrict__ row_of,
                                                           const float* __restrict__ wts, int T, int top_k,
                                                           uint16_t* __restrict__ y, int64_t ldy) {
   const int per_row = H / 8;
@@ -193,14 +200,21 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   float acc[8];
   for (int k = 0; k < top_k; ++k) {
     const float wk = wts[t * top_k + k];
-    const uint4 v = *reinterpret_cast<const uint4*>(z + static_cast<int64_t>(row_of[t * top_k + k]) * ldz + c);
-    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    const float* zr = z + static_cast<int64_t>(row_of[t * top_k + k]) * H + c;
+    float zv[8];
+    const float4 a0 = *reinterpret_cast<const float4*>(zr), a1 = *reinterpret_cast<const float4*>(zr + 4);
+    zv[0] = a0.x; zv[1] = a0.y; zv[2] = a0.z; zv[3] = a0.w; zv[4] = a1.x; zv[5] = a1.y; zv[6] = a1.z; zv[7] = a1.w;
+    for (int p = 1; p < kparts; ++p) {
+      const float4 b0 = *reinterpret_cast<const float4*>(zr + p * plane);
+      const float4 b1 = *reinterpret_cast<const float4*>(zr + p * plane + 4);
+      zv[0] = add_rn(zv[0], b0.x); zv[1] = add_rn(zv[1], b0.y); zv[2] = add_rn(zv[2], b0.z);
+      zv[3] = add_rn(zv[3], b0.w); zv[4] = add_rn(zv[4], b1.x); zv[5] = add_rn(zv[5], b1.y);
+      zv[6] = add_rn(zv[6], b1.z); zv[7] = add_rn(zv[7], b1.w);
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p0 = mul_rn(wk, bits_f32(w4[j] << 16));
-      const float p1 = mul_rn(wk, bits_f32(w4[j] & 0xffff0000u));
-      acc[2 * j] = k ? add_rn(acc[2 * j], p0) : p0;
-      acc[2 * j + 1] = k ? add_rn(acc[2 * j + 1], p1) : p1;
+    for (int j = 0; j < 8; ++j) {
+      const float p = mul_rn(wk, bf16_value(bf16_rne(zv[j])));
+      acc[j] = k ? add_rn(acc[j], p) : p;
     }
   }
   uint32_t o[4];
@@ -230,23 +244,24 @@ hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const in
   return hipGetLastError();
 }
 
-hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off, int E, int rows,
-                                 uint8_t* q, float* sa, bool half, hipStream_t stream) {
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off,
+                                 const int32_t* row_token, int E, int rows, uint8_t* q, float* sa, bool half,
+                                 hipStream_t stream) {
   const int G = inter / 128;
   const int64_t groups = static_cast<int64_t>(rows) * G;
   const int blocks = static_cast<int>((groups + 15) / 16);
   if (half)
-    silu_mul_quant_kernel<true><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, E, rows, q, sa);
+    silu_mul_quant_kernel<true><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa);
   else
-    silu_mul_quant_kernel<false><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, E, rows, q, sa);
+    silu_mul_quant_kernel<false><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa);
   return hipGetLastError();
 }
 
-hipError_t launch_moe_combine(const uint16_t* z, int64_t ldz, int H, const int32_t* row_of, const float* wts, int T,
-                              int top_k, uint16_t* y, int64_t ldy, hipStream_t stream) {
+hipError_t launch_moe_combine(const float* z, int kparts, int64_t plane, int H, const int32_t* row_of,
+                              const float* wts, int T, int top_k, uint16_t* y, int64_t ldy, hipStream_t stream) {
   const int64_t n = static_cast<int64_t>(T) * (H / 8);
-  moe_combine_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(z, ldz, H, row_of, wts, T, top_k,
-                                                                                   y, ldy);
+  moe_combine_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(z, kparts, plane, H, row_of, wts,
+                                                                                   T, top_k, y, ldy);
   return hipGetLastError();
 }
 

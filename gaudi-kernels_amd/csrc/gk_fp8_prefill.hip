@@ -61,9 +61,19 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
 }
 
 // Grouped (MoE) form: the rows of qa are expert segments starting at
-// group_off[e] (multiples of 256, group_off[n_groups] = rows in use); the
-// tile's rows belong to expert e, whose weights are w + e * w_stride and
-// scales sw + e * sw_stride.  Tiles past group_off[n_groups] exit at once.
+// group_off[e] (multiples of 256, group_off[n_groups] = rows in use) with
+// group_cnt[e] live rows; the tile's rows belong to expert e, whose weights
+// are w + e * w_stride and scales sw + e * sw_stride.  Tiles past
+// group_off[n_groups] exit at once.
+//
+// Live rows: a wave skips the MFMAs, fragment reads and stores of its 32-row
+// blocks that lie past the tile's live rows (rows >= M, or past the expert's
+// live rows): their outputs are never read.  The other wave of the SIMD then
+// has the matrix core to itself.
+//
+// fp32 output (yp != nullptr): the tile stores fp32 sums to yp[part][m][n]
+// instead of bf16 y (no bias).  K split (kparts = 2, grid doubled, needs yp):
+// the second half of the grid takes the second half of the groups.
 template <bool HALF, bool GROUPED>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
@@ -72,21 +82,31 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
                                                               const float* __restrict__ bias,
                                                               uint16_t* __restrict__ y, int64_t ldy, int M, int N,
                                                               int K, int G, int Mpad,
-                                                              const int32_t* __restrict__ group_off, int n_groups,
-                                                              int64_t w_stride, int64_t sw_stride) {
+                                                              const int32_t* __restrict__ group_off,
+                                                              const int32_t* __restrict__ group_cnt, int n_groups,
+                                                              int64_t w_stride, int64_t sw_stride, int kparts,
+                                                              float* __restrict__ yp) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
   const int wn = wave & 3, wm = wave >> 2;
   const int tiles_m = Mpad / kBM;
-  const int tn = static_cast<int>(blockIdx.x) / tiles_m, tm = static_cast<int>(blockIdx.x) % tiles_m;
+  const int tiles = tiles_m * ((N + kBN - 1) / kBN);
+  const int part = static_cast<int>(blockIdx.x) / tiles, bid = static_cast<int>(blockIdx.x) % tiles;
+  const int tn = bid / tiles_m, tm = bid % tiles_m;
   const int n0 = tn * kBN, m0 = tm * kBM;  // consecutive workgroups share the weight panel
+  int live = M - m0;                       // rows of this tile whose outputs are used
   if (GROUPED) {
     if (m0 >= group_off[n_groups]) return;  // uniform across the workgroup
     int e = 0;
     while (e + 1 < n_groups && group_off[e + 1] <= m0) ++e;
     w += e * w_stride;
     sw += e * sw_stride;
+    live = min(live, group_cnt[e] - (m0 - group_off[e]));
   }
+  // 32-row blocks of this wave's 128 rows that hold live rows (wave-uniform)
+  const int jlive = min(4, max(0, (live - wm * 128 + 31) / 32));
+  const int gbeg = (G * part) / kparts, gend = (G * (part + 1)) / kparts;
   const int64_t qstep = static_cast<int64_t>(Mpad) * 128;
 
   // Loader: wave w fills weight rows and activation rows [32 w, 32 w + 32) of
@@ -97,17 +117,24 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   int lcs[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ (((r0 + 8 * i) >> 1) & 7)) * 16;
+  // Per-lane 32-bit offsets from wave-uniform bases (the loads then use the
+  // scalar-base + 32-bit-offset form: fewer VGPRs than 64-bit pointers).
   const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;
   const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * 128;
   const int nmax = N - 1 - n0;
+  uint32_t aoff[4], boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    aoff[i] = static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
+    boff[i] = static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
+  }
   auto issue = [&](int g, int stage) {
     uint8_t* base = smem + stage * kStageBytes + wave * 32 * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = min(r0 + 8 * i, nmax);
-      __builtin_amdgcn_global_load_lds(asrc + static_cast<int64_t>(r) * K + static_cast<int64_t>(g) * 128 + lcs[i],
+      __builtin_amdgcn_global_load_lds(asrc + static_cast<uint64_t>(aoff[i] + static_cast<uint32_t>(g) * 128u),
                                        base + i * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(bsrc + static_cast<int64_t>(r0 + 8 * i) * 128 + g * qstep + lcs[i],
+      __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g * qstep)),
                                        base + kTile + i * 1024, 16, 0, 0);
     }
   };
@@ -129,9 +156,9 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  issue(0, 0);
-  for (int g = 0; g < G; ++g) {
-    const int stage = g & 1;
+  issue(gbeg, 0);
+  for (int g = gbeg; g < gend; ++g) {
+    const int stage = (g - gbeg) & 1;
     float sav[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) sav[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
@@ -139,7 +166,8 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     const float swg = HALF ? 2.0f * swp[g] : swp[g];
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of stage g (and everything older) are done
     __syncthreads();                // ... for every wave; all reads of stage g-1 are done too
-    if (g + 1 < G) issue(g + 1, stage ^ 1);
+    if (g + 1 < gend) issue(g + 1, stage ^ 1);
+    if (jlive == 0) continue;  // no live rows for this wave (it still takes part in the loads and barriers)
     const uint32_t A = lbase + stage * kStageBytes + arow;
     const uint32_t B = lbase + stage * kStageBytes + brow;
     v8i a00 = lds_frag(A + xo00, A + xo01), a01 = lds_frag(A + xo10, A + xo11);
@@ -151,34 +179,57 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (j > 0) {
-        b0 = lds_frag(B + j * 4096 + xo00, B + j * 4096 + xo01);
-        b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
-      }
-      const float f = sav[j] * swg;
-      v16f t0, t1;
+      if (j < jlive) {  // wave-uniform; j is a constant after unrolling, so acc stays in registers
+        if (j > 0) {
+          b0 = lds_frag(B + j * 4096 + xo00, B + j * 4096 + xo01);
+          b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
+          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
+        }
+        const float f = sav[j] * swg;
+        v16f t0, t1;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) { t0[r] = 0.0f; t1[r] = 0.0f; }
-      t0 = mfma32_f8(a00, b0, t0);
-      t1 = mfma32_f8(a10, b0, t1);
-      t0 = mfma32_f8(a01, b1, t0);
-      t1 = mfma32_f8(a11, b1, t1);
-      promote(acc[0][j], t0, f);
-      promote(acc[1][j], t1, f);
+        for (int r = 0; r < 16; ++r) { t0[r] = 0.0f; t1[r] = 0.0f; }
+        t0 = mfma32_f8(a00, b0, t0);
+        t1 = mfma32_f8(a10, b0, t1);
+        t0 = mfma32_f8(a01, b1, t0);
+        t1 = mfma32_f8(a11, b1, t1);
+        promote(acc[0][j], t0, f);
+        promote(acc[1][j], t1, f);
+      }
     }
   }
 
+  if (yp) {
+    float* ypp = yp + static_cast<int64_t>(part) * M * N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j < jlive) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int m = m0 + wm * 128 + j * 32 + fr, n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+            if (m < M && n < N)  // N % 4 == 0 here
+              *reinterpret_cast<v4f*>(ypp + static_cast<int64_t>(m) * N + n) =
+                  v4f{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          }
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      if (j < jlive) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-        store_tile(y, ldy, bias, M, N, m0 + wm * 128 + j * 32 + fr, n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5),
-                   v);
+        for (int q = 0; q < 4; ++q) {
+          const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          store_tile(y, ldy, bias, M, N, m0 + wm * 128 + j * 32 + fr,
+                     n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5), v);
+        }
       }
+    }
 }
 
 // The 128 KB of dynamic LDS is above the default limit: raise it once per device.
@@ -203,14 +254,14 @@ hipError_t ensure_lds_limit() {
 }
 
 template <bool HALF, bool GROUPED>
-hipError_t launch256(const GemmArgs& a, const int32_t* group_off, int n_groups, int64_t w_stride,
-                     int64_t sw_stride, hipStream_t stream) {
+hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
+                     int64_t w_stride, int64_t sw_stride, int kparts, float* yp, hipStream_t stream) {
   hipError_t e = ensure_lds_limit<HALF, GROUPED>();
   if (e != hipSuccess) return e;
   const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
-  gemm_prefill256_kernel<HALF, GROUPED><<<tiles, 512, kLdsBytes, stream>>>(
-      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, n_groups, w_stride,
-      sw_stride);
+  gemm_prefill256_kernel<HALF, GROUPED><<<tiles * kparts, 512, kLdsBytes, stream>>>(
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
+      w_stride, sw_stride, kparts, yp);
   return hipGetLastError();
 }
 
@@ -219,19 +270,23 @@ hipError_t launch256(const GemmArgs& a, const int32_t* group_off, int n_groups, 
 // Requires K % 128 == 0, 16-byte aligned weights, Mpad % 256 == 0 (qa/sa
 // padded with zero rows up to Mpad).
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
-  if (a.Mpad % kBM != 0) return hipErrorInvalidValue;
-  return a.half_w ? launch256<true, false>(a, nullptr, 0, 0, 0, stream)
-                  : launch256<false, false>(a, nullptr, 0, 0, 0, stream);
+  if (a.Mpad % kBM != 0 || !prefill256_fits(a)) return hipErrorInvalidValue;
+  return a.half_w ? launch256<true, false>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream)
+                  : launch256<false, false>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream);
 }
 
 // Grouped form: a.Mpad = padded rows (multiple of 256), a.M = a.Mpad; weights
-// [n_groups][N][K], scales [n_groups][ceil(N/128)][G]; group_off on device.
-hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, int n_groups, hipStream_t stream) {
-  if (a.Mpad % kBM != 0 || n_groups < 1) return hipErrorInvalidValue;
+// [n_groups][N][K], scales [n_groups][ceil(N/128)][G]; group_off, group_cnt on device.
+hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt,
+                                  int n_groups, int kparts, float* yp, hipStream_t stream) {
+  if (a.Mpad % kBM != 0 || n_groups < 1 || kparts < 1 || kparts > 2 || (kparts > 1 && !yp) || (yp && a.N % 4) ||
+      !prefill256_fits(a))
+    return hipErrorInvalidValue;
   const int64_t w_stride = static_cast<int64_t>(a.N) * a.K;
   const int64_t sw_stride = static_cast<int64_t>((a.N + 127) / 128) * a.G;
-  return a.half_w ? launch256<true, true>(a, group_off, n_groups, w_stride, sw_stride, stream)
-                  : launch256<false, true>(a, group_off, n_groups, w_stride, sw_stride, stream);
+  return a.half_w ? launch256<true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, stream)
+                  : launch256<false, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
+                                           stream);
 }
 
 }  // namespace gk

@@ -104,20 +104,27 @@ def test_moe_strided_output_and_reuse():
 def regions(ws, t, h, inter, e, k):
     """Views of the workspace regions documented for gk_fp8_moe_bf16 (include/gk_fp8.h)."""
     rows = ops.moe_rows_max(t, e, k)
+    parts = 2 if (rows // 256) * ((h + 255) // 256) < 512 else 1
     sizes = [("ids", t * k * 4), ("wts", t * k * 4), ("row_of", t * k * 4), ("row_token", rows * 4),
-             ("off", (e + 1) * 4), ("q1", rows * h), ("sa1", rows * h // 128 * 4), ("hpre", rows * 2 * inter * 2),
-             ("q2", rows * inter), ("sa2", rows * inter // 128 * 4), ("z", rows * h * 2)]
+             ("off", (e + 1) * 4), ("cnt", e * 4), ("q1", rows * h), ("sa1", rows * h // 128 * 4),
+             ("hpre", rows * 2 * inter * 2), ("q2", rows * inter), ("sa2", rows * inter // 128 * 4),
+             ("z", parts * rows * h * 4)]
     out, at = {}, 0
     for name, nbytes in sizes:
         out[name] = ws[at:at + nbytes]
         at += (nbytes + 255) // 256 * 256
     assert at == ops.moe_workspace_bytes(t, h, inter, e, k)
-    v = {n: out[n].view(torch.int32) for n in ("ids", "row_of", "row_token", "off")}
+    v = {n: out[n].view(torch.int32) for n in ("ids", "row_of", "row_token", "off", "cnt")}
     v["wts"] = out["wts"].view(torch.float32)
     v["hpre"] = out["hpre"].view(torch.bfloat16).reshape(rows, 2 * inter)
-    v["z"] = out["z"].view(torch.bfloat16).reshape(rows, h)
     v["q2"] = out["q2"].reshape(inter // 128, rows, 128)
     v["sa2"] = out["sa2"].view(torch.float32).reshape(inter // 128, rows)
+    zp = out["z"].view(torch.float32).reshape(parts, rows, h)
+    z = zp[0].clone()
+    for p in range(1, parts):
+        z = z + zp[p]                     # fp32, as the combine does
+    v["z"] = z.to(torch.bfloat16)
+    v["parts"] = torch.tensor(parts)
     return {n: x.cpu() for n, x in v.items()}
 
 
@@ -136,6 +143,8 @@ def test_moe_config5_stagewise_parity():
     r = regions(ws, t, h, inter, e, k)
     ids = r["ids"].reshape(t, k)
     row_of = r["row_of"].reshape(t, k).long()
+    assert torch.equal(r["cnt"].long(), torch.bincount(ids.reshape(-1).long(), minlength=e))
+    assert int(r["parts"]) == 2  # config 5: the down GEMM splits K
     tokens = torch.randperm(t, generator=torch.Generator().manual_seed(2))[:12]
     for x_e in range(e):
         pairs = [(int(tok), s) for tok in tokens for s in range(k) if int(ids[tok, s]) == x_e]
