@@ -26,6 +26,8 @@ constexpr const char* kOps[] = {
     "gk_fp8_block_gemm_bf16_v1",    // quant -> MME -> reduce_bias.c / prefill chain, fused
     "gk_fp8_block_gemm_q_bf16_v1",  // GEMM on pre-quantized activations
     "gk_fp8_check_inputs_v1",       // block_fp8_oracle.py:22-24
+    "gk_silu_and_mul_bf16_v1",      // silu_and_mul_bf16.c, glue generic_dense_glue.cpp:196-236
+    "gk_fp8_silu_mul_quant_bf16_v1",  // SiLU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
     "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (build-defined)
 };
@@ -345,6 +347,42 @@ gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, 
   st = read_status(workspace, &stat, s);
   if (st != GK_SUCCESS) return st;
   return stat.flags ? GK_NONFINITE_INPUT : GK_SUCCESS;
+}
+
+// ---- SiLU-and-mul ----------------------------------------------------------------------
+gk_status gk_silu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* out,
+                               int64_t ld_out, void* stream) {
+  if (!gate_up || !out) return GK_INVALID_ARGUMENT;
+  // generic_dense_glue.cpp:203-210: nonzero sizes within int, input width even (= 2 * width)
+  if (rows < 1 || width < 1 || rows > kMaxDim || width > kMaxDim / 2 || ld_in < 2 * width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ld_out < width) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(gate_up) | reinterpret_cast<uintptr_t>(out)) & 1) return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_silu_and_mul(static_cast<const uint16_t*>(gate_up), ld_in, static_cast<int>(rows),
+                                          static_cast<int>(width), static_cast<uint16_t*>(out), ld_out,
+                                          static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* q,
+                                     float* sa, int64_t m_pad, uint32_t flags, void* stream) {
+  if (!gate_up || !q || !sa) return GK_INVALID_ARGUMENT;
+  if (rows < 1 || width < 1 || rows > kMaxDim || width > kMaxDim / 2 || ld_in < 2 * width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (m_pad < rows || m_pad > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_DECODE_LAYOUT}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
+  if (packed && m_pad != gk::kDecodeMaxRows) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(gate_up) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
+      (reinterpret_cast<uintptr_t>(sa) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_silu_mul_act_quant(static_cast<const uint16_t*>(gate_up), ld_in, static_cast<int>(rows),
+                                                static_cast<int>(width), static_cast<int>(m_pad),
+                                                static_cast<uint8_t*>(q), sa, (flags & GK_FLAG_NATIVE_HALF) != 0,
+                                                packed, static_cast<hipStream_t>(stream)));
 }
 
 // ---- MoE ------------------------------------------------------------------------------

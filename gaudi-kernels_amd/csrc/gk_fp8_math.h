@@ -94,6 +94,17 @@ __host__ __device__ inline float add_rn(float a, float b) {
   return a + b;
 }
 
+// SiLU of the reference's fused SiLU-and-mul (csrc/tpc/generic_dense/
+// silu_and_mul_bf16.c:4-15): g / (1 + e^-g) in fp32; g <= -88 gives 0; NaN
+// passes through; g = +inf gives NaN there (its Newton-refined quotient
+// computes -inf + inf), and so here.  The quotient is the IEEE one.
+__host__ __device__ inline float silu_ref(float g) {
+  if (g != g) return g;
+  if (g <= -88.0f) return 0.0f;
+  if (g == __builtin_huge_valf()) return __builtin_nanf("");
+  return g / (1.0f + expf(-g));
+}
+
 __host__ __device__ inline uint16_t bf16_rne(float v) {
   const uint32_t b = f32_bits(v);
   if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;

@@ -145,12 +145,6 @@ __global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __r
 // h: bf16 [rows, 2*inter] (gate | up); rows past off[E] and padding rows
 // (row_token < 0, whose gate_up outputs were never computed) are skipped.
 // Lane: 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
-__device__ inline float silu_f32(float g) {
-  if (g <= -88.0f) return 0.0f;                 // silu_and_mul_bf16.c:10
-  if (!(fabsf(g) <= 3.4028235e38f)) return g;   // NaN / inf pass through (:11-12)
-  return g / (1.0f + expf(-g));
-}
-
 template <bool HALF>
 __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ h, int64_t ldh, int inter,
                                                              int G, const int32_t* __restrict__ off,
@@ -174,8 +168,8 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __r
   for (int i = 0; i < 4; ++i) {
     const float g0 = bits_f32(gw[i] << 16), g1 = bits_f32(gw[i] & 0xffff0000u);
     const float u0 = bits_f32(uw[i] << 16), u1 = bits_f32(uw[i] & 0xffff0000u);
-    const uint32_t p0 = bf16_rne(mul_rn(silu_f32(g0), u0));
-    const uint32_t p1 = bf16_rne(mul_rn(silu_f32(g1), u1));
+    const uint32_t p0 = bf16_rne(mul_rn(silu_ref(g0), u0));
+    const uint32_t p1 = bf16_rne(mul_rn(silu_ref(g1), u1));
     out[i] = p0 | (p1 << 16);
   }
   float s;

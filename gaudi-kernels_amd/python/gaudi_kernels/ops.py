@@ -246,6 +246,44 @@ def inputs_finite(x, weight, scales):
     return True
 
 
+def _check_gate_up(gate_up, device):
+    if gate_up.dtype != torch.bfloat16 or gate_up.ndim != 2 or gate_up.stride(1) != 1 or gate_up.shape[1] % 2:
+        raise ValueError("expected a 2-D bf16 gate_up [rows, 2*width] with unit column stride")
+    if gate_up.device != device:
+        raise ValueError("gate_up must be on the GPU")
+    return gate_up.shape[0], gate_up.shape[1] // 2
+
+
+def silu_and_mul(gate_up, *, out=None):
+    """bf16 [rows, 2W] (gate | up) -> bf16 [rows, W] = bf16(silu(gate) * up) (gk_silu_and_mul_bf16_v1)."""
+    device = require_device(gate_up.device)
+    rows, width = _check_gate_up(gate_up, device)
+    if out is None:
+        out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    elif out.dtype != torch.bfloat16 or out.shape != (rows, width) or out.stride(1) != 1 or out.device != device:
+        raise ValueError("out must be bf16 [rows, W] with unit column stride on the same GPU")
+    nat.check("gk_silu_and_mul_bf16",
+              nat.load().gk_silu_and_mul_bf16(_ptr(gate_up), rows, width, gate_up.stride(0), _ptr(out),
+                                              out.stride(0), _stream(device)))
+    return out
+
+
+def silu_mul_quant(gate_up, *, native_half=False, m_pad=None, decode_layout=False):
+    """SiLU-and-mul fused with the 1x128 quantizer -> (codes [G, m_pad, 128], sa [G, m_pad]) as act_quant
+    of silu_and_mul(gate_up) would give; decode_layout as in act_quant."""
+    device = require_device(gate_up.device)
+    rows, width = _check_gate_up(gate_up, device)
+    g = (width + 127) // 128
+    m_pad = (16 if decode_layout else rows) if m_pad is None else m_pad
+    q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
+    sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
+    flags = (nat.GK_FLAG_NATIVE_HALF if native_half else 0) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
+    nat.check("gk_fp8_silu_mul_quant_bf16",
+              nat.load().gk_fp8_silu_mul_quant_bf16(_ptr(gate_up), rows, width, gate_up.stride(0), _ptr(q),
+                                                    _ptr(sa), m_pad, flags, _stream(device)))
+    return q, sa
+
+
 def moe_rows_max(tokens, n_experts, top_k=2):
     """Padded row count of the expert-sorted layout (an upper bound of the rows in use)."""
     rows = ctypes.c_int64(0)

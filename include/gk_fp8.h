@@ -159,6 +159,26 @@ gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, 
                               const float* scales, int64_t n_scales, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* ---- SiLU-and-mul ------------------------------------------------------------ */
+
+/* The reference's gk_silu_and_mul_bf16_v1 (csrc/tpc/generic_dense/
+ * silu_and_mul_bf16.c, glue generic_dense_glue.cpp:196-236): gate_up bf16
+ * [rows, 2*width] (gate = columns [0, width), up = [width, 2*width), row
+ * stride ld_in >= 2*width) -> out bf16 [rows, width] (row stride ld_out),
+ * out = bf16(silu(gate) * up) in fp32, silu(g) = g / (1 + e^-g), g <= -88 ->
+ * 0, NaN -> NaN, +inf -> NaN. */
+gk_status gk_silu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* out,
+                               int64_t ld_out, void* stream);
+
+/* The same products quantized per 1x128 group for the next block-FP8 GEMM
+ * (no reference op: the fusion SURVEY ranks first among the path's
+ * neighbours): codes and scales exactly as gk_fp8_act_quant_bf16 would write
+ * for the bf16 output of gk_silu_and_mul_bf16 (q [G][m_pad][128], sa
+ * [G][m_pad], G = ceil(width/128); flags GK_FLAG_NATIVE_HALF,
+ * GK_FLAG_DECODE_LAYOUT with m_pad = 16). */
+gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* q,
+                                     float* sa, int64_t m_pad, uint32_t flags, void* stream);
+
 /* ---- block-FP8 MoE layer ------------------------------------
  * No reference function: the reference has no MoE code for this path.  The
  * layer is build-defined from the reference's pieces (oracle/moe.py restates

@@ -16,8 +16,9 @@ pieces:
            -- python/gaudi_kernels/block_fp8_oracle.py:11-46, bf16 out.
   act      h = bf16(silu(gate) * up) in fp32, gate = first half of the
            columns, up = second half, silu(g) = g / (1 + exp(-g)), g <= -88
-           -> 0; only the product is rounded -- the semantics of the
-           reference's fused SiLU-and-mul kernel
+           -> 0, NaN -> NaN, +inf -> NaN (the reference's Newton-refined
+           quotient computes -inf + inf there); only the product is rounded
+           -- the semantics of the reference's fused SiLU-and-mul kernel
            (csrc/tpc/generic_dense/silu_and_mul_bf16.c:4-15, 15-16).
   down     z_e = block_fp8_oracle.reference(h, W_dn[e], S_dn[e]), bf16.
   combine  y[t] = bf16(sum_k w[t, k] * z[row(t, k)]) in fp32, k ascending.
@@ -105,6 +106,7 @@ def silu_mul(gate_up):
     u = gate_up[:, gate_up.shape[1] // 2:].float()
     s = g / (1.0 + torch.exp(-g))
     s = torch.where(g <= -88.0, torch.zeros_like(s), s)
+    s = torch.where(g == float("inf"), torch.full_like(s, float("nan")), s)  # silu_and_mul_bf16.c:8-9
     return (s * u).to(torch.bfloat16)
 
 

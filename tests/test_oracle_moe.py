@@ -82,13 +82,16 @@ def test_silu_mul_against_fp64_and_special_cases():
     want = moe.silu_mul_f64(gu)
     # one bf16 rounding of a value within a few fp32 ulps of the fp64 result
     assert torch.all((got - want).abs() <= want.abs() * 2.0 ** -8 + 1e-30)
-    g = torch.tensor([[0.0, -88.0, -100.0, 200.0, 1.0, -87.5]]).bfloat16()
-    u = torch.tensor([[3.0, 5.0, 5.0, 2.0, 1.0, 1e30]]).bfloat16()
+    inf, nan = float("inf"), float("nan")
+    g = torch.tensor([[0.0, -88.0, -100.0, 200.0, 1.0, -87.5, inf, -inf, nan]]).bfloat16()
+    u = torch.tensor([[3.0, 5.0, 5.0, 2.0, 1.0, 1e30, 1.0, 1.0, 1.0]]).bfloat16()
     out = moe.silu_mul(torch.cat([g, u], 1)).float()[0]
     assert out[0] == 0 and out[1] == 0 and out[2] == 0
     assert out[3] == float(torch.tensor(400.0).bfloat16())                  # silu(g) = g for large g
     assert out[4] == float(torch.tensor(1.0 / (1.0 + np.exp(-1.0))).bfloat16())
     assert out[5] != 0                                                       # -87.5 is above the cutoff
+    # silu_and_mul_bf16.c:8-12: +inf -> (-inf + inf) = NaN; -inf <= -88 -> 0; NaN passes through
+    assert torch.isnan(out[6]) and out[7] == 0 and torch.isnan(out[8])
 
 
 def _small_problem(t, h, inter, e, seed):
