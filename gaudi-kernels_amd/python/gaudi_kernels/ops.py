@@ -359,3 +359,9 @@ def moe_block_fp8(x, logits, w_gate_up, s_gate_up, w_down, s_down, *, top_k=2, n
                                          nat.GK_FLAG_NATIVE_HALF if native_half else 0, _ptr(ws), ws.numel(),
                                          _stream(device)))
     return out
+
+
+def weights_finite(weight, scales):
+    """True iff the E4M3FN weight holds no NaN code and its scales are finite and >= 0 (GPU check)."""
+    x = torch.zeros((1, weight.shape[-1]), dtype=torch.bfloat16, device=weight.device)
+    return inputs_finite(x, weight.reshape(-1, weight.shape[-1]), scales)
