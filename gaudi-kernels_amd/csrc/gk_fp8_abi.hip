@@ -26,6 +26,9 @@ constexpr const char* kOps[] = {
     "gk_fp8_block_gemm_bf16_v1",    // quant -> MME -> reduce_bias.c / prefill chain, fused
     "gk_fp8_block_gemm_q_bf16_v1",  // GEMM on pre-quantized activations
     "gk_fp8_check_inputs_v1",       // block_fp8_oracle.py:22-24
+    "gk_fp8_token_quant_bf16_v1",   // activation_token.c:4-26, glue generic_fp8_glue.hpp:31-50
+    "gk_fp8_channel_finish_bf16_v1",  // channel_finish.c:2-18, glue generic_fp8_glue.hpp:52-82
+    "gk_fp8_channel_gemm_bf16_v1",  // MME + channel finish, fused (build-defined)
     "gk_silu_and_mul_bf16_v1",      // silu_and_mul_bf16.c, glue generic_dense_glue.cpp:196-236
     "gk_fp8_silu_mul_quant_bf16_v1",  // SiLU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
@@ -347,6 +350,67 @@ gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, 
   st = read_status(workspace, &stat, s);
   if (st != GK_SUCCESS) return st;
   return stat.flags ? GK_NONFINITE_INPUT : GK_SUCCESS;
+}
+
+// ---- per-token / per-channel ----------------------------------------------------------
+gk_status gk_fp8_token_quant_bf16(const void* x, int64_t rows, int64_t width, int64_t ldx, void* q, int64_t ldq,
+                                  float* scales, void* stream) {
+  if (!x || !q || !scales) return GK_INVALID_ARGUMENT;
+  // generic_fp8_glue.hpp:39-44: nonzero width, multiple of 128; rows >= 1
+  if (rows < 1 || width < 128 || width % 128 || rows > kMaxDim || width > kMaxDim || ldx < width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldq < width || ldq % 8) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(x) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
+      (reinterpret_cast<uintptr_t>(scales) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_token_quant(static_cast<const uint16_t*>(x), ldx, static_cast<int>(rows),
+                                         static_cast<int>(width), static_cast<uint8_t*>(q), ldq, scales,
+                                         static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_channel_finish_bf16(const float* partial, int64_t rows, int64_t width, int64_t ldp,
+                                     const float* act_scales, const float* w_scales, const float* bias, void* y,
+                                     int64_t ldy, void* stream) {
+  if (!partial || !act_scales || !w_scales || !y) return GK_INVALID_ARGUMENT;
+  // generic_fp8_glue.hpp:61-66: width a nonzero multiple of 128
+  if (rows < 1 || width < 128 || width % 128 || rows > kMaxDim || width > kMaxDim || ldp < width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldy < width) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (((reinterpret_cast<uintptr_t>(partial) | reinterpret_cast<uintptr_t>(act_scales) |
+        reinterpret_cast<uintptr_t>(w_scales) | reinterpret_cast<uintptr_t>(bias)) & 3) ||
+      (reinterpret_cast<uintptr_t>(y) & 1))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_channel_finish(partial, ldp, static_cast<int>(rows), static_cast<int>(width),
+                                            act_scales, w_scales, bias, static_cast<uint16_t*>(y), ldy,
+                                            static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_channel_gemm_bf16(const void* q, int64_t ldq, const float* sa, int64_t m, int64_t k, const void* w,
+                                   int64_t n, const float* sw, const float* bias, void* y, int64_t ldy,
+                                   uint32_t flags, void* stream) {
+  if (!q || !sa || !w || !sw || !y) return GK_INVALID_ARGUMENT;
+  if (flags) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (m < 1 || n < 1 || k < 128 || k % 128 || m > kMaxDim || n > kMaxDim || k > kMaxDim || ldq < k)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldy < n) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(w)) & 15) || ldq % 16 ||
+      ((reinterpret_cast<uintptr_t>(sa) | reinterpret_cast<uintptr_t>(sw) | reinterpret_cast<uintptr_t>(bias)) & 3) ||
+      (reinterpret_cast<uintptr_t>(y) & 1))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  if (int64_t{256} * ldq > int64_t{0xffffffff} || int64_t{256} * k > int64_t{0xffffffff})
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  gk::GemmArgs a{};
+  a.qa = static_cast<const uint8_t*>(q); a.sa = sa; a.w = static_cast<const uint8_t*>(w); a.sw = sw; a.bias = bias;
+  a.y = static_cast<uint16_t*>(y); a.ldy = ldy; a.M = static_cast<int>(m); a.N = static_cast<int>(n);
+  a.K = static_cast<int>(k); a.G = static_cast<int>(k / 128); a.Mpad = static_cast<int>(m); a.half_w = false;
+  a.channel = true; a.ldq = ldq;
+  return from_hip(gk::launch_gemm_channel(a, static_cast<hipStream_t>(stream)));
 }
 
 // ---- SiLU-and-mul ----------------------------------------------------------------------

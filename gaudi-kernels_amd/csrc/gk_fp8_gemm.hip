@@ -54,14 +54,19 @@ namespace gk {
 // touches fewer activation lines.  Every load is unconditional (indices are
 // clamped) and all loads of a step are issued before the first use: the
 // compiler then waits on them one by one instead of draining the queue.
-template <int NW, int R, int U, bool HALF, bool QPACK>
+//
+// CH (per-token / per-channel scaling): activations row-major [M][ldq], one
+// scale per token sa[m] and per output channel sw[n]; the MFMAs accumulate
+// over all of K (no per-group promotion) and the epilogue applies
+// bf16(fma(p * sa[m], sw[n], bias[n])) (channel_finish.c:9-15).
+template <int NW, int R, int U, bool HALF, bool QPACK, bool CH = false>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
                                                               const float* __restrict__ sw,
                                                               const float* __restrict__ bias,
                                                               uint16_t* __restrict__ y, int64_t ldy, int M,
-                                                              int N, int K, int G) {
+                                                              int N, int K, int G, int64_t ldq = 0) {
   static_assert(16 * R <= 128 && NW >= R, "a workgroup's rows lie in one 128-row scale block");
   __shared__ __attribute__((aligned(16))) uint8_t tile[NW][2048];
   __shared__ v4f red[NW][R][64];
@@ -83,8 +88,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   const uint32_t roff0 = col * 128 + (((2 * quad) ^ ((col >> 1) & 7)) << 4);
   const uint32_t roff1 = col * 128 + (((2 * quad + 1) ^ ((col >> 1) & 7)) << 4);
   const int tok = min(col, M - 1);
-  const uint8_t* qp = QPACK ? qa + (16 * quad + tok) * 16 : qa + tok * 128 + quad * 32;
+  const uint8_t* qp = CH      ? qa + tok * ldq + quad * 32
+                      : QPACK ? qa + (16 * quad + tok) * 16
+                              : qa + tok * 128 + quad * 32;
   constexpr int kQHi = QPACK ? 1024 : 16;
+  constexpr int kQG = CH ? 128 : 2048;              // bytes from one group to the next
   const float* sap = sa + tok;                      // + g * 16
   const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
@@ -105,29 +113,36 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
         wa[u][r][0] = load_stream16(p);
         wa[u][r][1] = load_stream16(p + d8[r]);
       }
-      const uint8_t* q = qp + static_cast<int64_t>(g) * 2048;
+      const uint8_t* q = qp + static_cast<int64_t>(g) * kQG;
       qb[u][0] = *reinterpret_cast<const uint4*>(q);
       qb[u][1] = *reinterpret_cast<const uint4*>(q + kQHi);
-      sv[u] = sap[g * 16];
-      wv[u] = swp[g];
+      if (!CH) {
+        sv[u] = sap[g * 16];
+        wv[u] = swp[g];
+      }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the step is in flight before the first use
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const v8i b = pack8(qb[u][0], qb[u][1]);
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-      const float f = (g0 + u < gend) ? sv[u] * (HALF ? 2.0f * wv[u] : wv[u]) : 0.0f;
+      const float f = CH ? 0.0f : (g0 + u < gend) ? sv[u] * (HALF ? 2.0f * wv[u] : wv[u]) : 0.0f;
+      const bool live = g0 + u < gend;  // the clamped repeat of the last group adds nothing
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         *reinterpret_cast<uint4*>(buf + woff0) = wa[u][r][0];
         *reinterpret_cast<uint4*>(buf + woff1) = wa[u][r][1];
         const uint4 lo = *reinterpret_cast<const uint4*>(buf + roff0);
         const uint4 hi = *reinterpret_cast<const uint4*>(buf + roff1);
-        const v4f t = mfma_f8(weight_frag<HALF>(lo, hi), b);
-        acc[r][0] = fmaf(t[0], f, acc[r][0]);
-        acc[r][1] = fmaf(t[1], f, acc[r][1]);
-        acc[r][2] = fmaf(t[2], f, acc[r][2]);
-        acc[r][3] = fmaf(t[3], f, acc[r][3]);
+        if (CH) {
+          if (live) acc[r] = mfma_f8_acc(weight_frag<HALF>(lo, hi), b, acc[r]);
+        } else {
+          const v4f t = mfma_f8(weight_frag<HALF>(lo, hi), b);
+          acc[r][0] = fmaf(t[0], f, acc[r][0]);
+          acc[r][1] = fmaf(t[1], f, acc[r][1]);
+          acc[r][2] = fmaf(t[2], f, acc[r][2]);
+          acc[r][3] = fmaf(t[3], f, acc[r][3]);
+        }
       }
     }
   }
@@ -138,6 +153,16 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   v4f sum = red[0][wave][lane];
 #pragma unroll
   for (int v = 1; v < NW; ++v) sum += red[v][wave][lane];
+  if (CH) {
+    const int n = n0 + 16 * wave + 4 * quad;
+    if (col >= M) return;
+    const float sam = sa[col];
+    uint16_t* row = y + static_cast<int64_t>(col) * ldy + n;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) row[r] = channel_out(sum[r], sam, sw[n + r], bias ? bias[n + r] : 0.0f);
+    return;
+  }
   store_tile(y, ldy, bias, M, N, col, n0 + 16 * wave + 4 * quad, sum);
 }
 
@@ -319,6 +344,14 @@ DecodeShape plan_decode_shape(int N, int G) {
   return DecodeShape{16, 1};
 }
 
+template <int NW, int R, int U>
+static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
+  gemm_decode_kernel<NW, R, U, false, false, true><<<grid, NW * 64, 0, stream>>>(
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
   const int key = a.dec.nw * 10 + a.dec.r;
   switch (key) {
@@ -341,6 +374,17 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
     gemm_prefill_kernel<false><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,
                                                          a.K, a.G, a.Mpad);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream) {
+  if (a.M > kDecodeMaxRows) return launch_gemm_channel256(a, stream);
+  const DecodeShape d = plan_decode_shape(a.N, a.G);
+  switch (d.nw * 10 + d.r) {
+    case 44: return decode_channel_launch<4, 4, 4>(a, stream);
+    case 82: return decode_channel_launch<8, 2, 2>(a, stream);
+    case 161: return decode_channel_launch<16, 1, 2>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream) {

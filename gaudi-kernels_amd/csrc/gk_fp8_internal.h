@@ -89,6 +89,10 @@ struct GemmArgs {
   bool half_w;        // native_half: half-range codec on weight codes in-kernel, weight scales x2
   DecodeShape dec;    // decode variant only
   bool qpack = false; // decode variant only: qa in the packed decode layout (launch_act_quant packed)
+  // Per-token / per-channel scaling (launch_gemm_channel): qa row-major [M][ldq]
+  // codes, sa [M] per token, sw [N] per output channel, no per-group promotion.
+  bool channel = false;
+  int64_t ldq = 0;
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
@@ -109,6 +113,20 @@ inline bool prefill256_fits(const GemmArgs& a) {
 hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt,
                                   int n_groups, int kparts, float* yp, hipStream_t stream);
 hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream);
+// Per-token / per-channel GEMM (a.channel): M <= 16 streams weights (decode
+// shapes), larger M runs the 256 x 256 kernel in its channel form.
+hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream);
+hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream);  // gk_fp8_prefill.hip
+
+// ---- per-token activation quantization (gk_fp8_token.hip) ------------------------
+// activation_token.c:4-26: q [rows][width] Gaudi2 half-range codes (row-major,
+// row stride ldq), scales [rows] = 2 * fp8_activation_scale(row max |x|).
+hipError_t launch_token_quant(const uint16_t* x, int64_t ldx, int rows, int width, uint8_t* q, int64_t ldq,
+                              float* scales, hipStream_t stream);
+// channel_finish.c:2-18 on an fp32 partial [rows][width].
+hipError_t launch_channel_finish(const float* partial, int64_t ldp, int rows, int width, const float* act_scales,
+                                 const float* w_scales, const float* bias, uint16_t* y, int64_t ldy,
+                                 hipStream_t stream);
 
 // ---- SiLU-and-mul (gk_fp8_act.hip) -------------------------------------------
 // in: bf16 [rows, 2*width] (gate | up), row stride ldi; out bf16 [rows, width].

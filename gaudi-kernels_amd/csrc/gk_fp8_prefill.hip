@@ -74,7 +74,12 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
 // fp32 output (yp != nullptr): the tile stores fp32 sums to yp[part][m][n]
 // instead of bf16 y (no bias).  K split (kparts = 2, grid doubled, needs yp):
 // the second half of the grid takes the second half of the groups.
-template <bool HALF, bool GROUPED>
+//
+// CH (per-token / per-channel scaling): activations row-major [M][ldq] (rows
+// past M re-read row M-1), sa [M], sw [N]; the MFMAs accumulate over all of
+// K and the epilogue applies bf16(fma(p * sa[m], sw[n], bias[n]))
+// (channel_finish.c:9-15).
+template <bool HALF, bool GROUPED, bool CH = false>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -85,7 +90,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
                                                               const int32_t* __restrict__ group_off,
                                                               const int32_t* __restrict__ group_cnt, int n_groups,
                                                               int64_t w_stride, int64_t sw_stride, int kparts,
-                                                              float* __restrict__ yp) {
+                                                              float* __restrict__ yp, int64_t ldq = 0) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
@@ -120,13 +125,15 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   // Per-lane 32-bit offsets from wave-uniform bases (the loads then use the
   // scalar-base + 32-bit-offset form: fewer VGPRs than 64-bit pointers).
   const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;
-  const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * 128;
-  const int nmax = N - 1 - n0;
+  const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * (CH ? ldq : 128);
+  const int nmax = N - 1 - n0, mmax = M - 1 - m0;
+  const uint32_t gstep = CH ? 128u : static_cast<uint32_t>(qstep);  // activation bytes from group to group
   uint32_t aoff[4], boff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     aoff[i] = static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
-    boff[i] = static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
+    boff[i] = CH ? static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i])
+                 : static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
   }
   auto issue = [&](int g, int stage) {
     uint8_t* base = smem + stage * kStageBytes + wave * 32 * 128;
@@ -134,7 +141,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     for (int i = 0; i < 4; ++i) {
       __builtin_amdgcn_global_load_lds(asrc + static_cast<uint64_t>(aoff[i] + static_cast<uint32_t>(g) * 128u),
                                        base + i * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g * qstep)),
+      __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g) * gstep),
                                        base + kTile + i * 1024, 16, 0, 0);
     }
   };
@@ -159,11 +166,13 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   issue(gbeg, 0);
   for (int g = gbeg; g < gend; ++g) {
     const int stage = (g - gbeg) & 1;
-    float sav[4];
+    float sav[4] = {0.0f, 0.0f, 0.0f, 0.0f}, swg = 0.0f;
+    if (!CH) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sav[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
-    // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-    const float swg = HALF ? 2.0f * swp[g] : swp[g];
+      for (int j = 0; j < 4; ++j) sav[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
+      // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
+      swg = HALF ? 2.0f * swp[g] : swp[g];
+    }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of stage g (and everything older) are done
     __syncthreads();                // ... for every wave; all reads of stage g-1 are done too
     if (g + 1 < gend) issue(g + 1, stage ^ 1);
@@ -185,20 +194,50 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
           b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
           asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
         }
-        const float f = sav[j] * swg;
-        v16f t0, t1;
+        if (CH) {
+          acc[0][j] = mfma32_f8(a00, b0, acc[0][j]);
+          acc[1][j] = mfma32_f8(a10, b0, acc[1][j]);
+          acc[0][j] = mfma32_f8(a01, b1, acc[0][j]);
+          acc[1][j] = mfma32_f8(a11, b1, acc[1][j]);
+        } else {
+          const float f = sav[j] * swg;
+          v16f t0, t1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) { t0[r] = 0.0f; t1[r] = 0.0f; }
-        t0 = mfma32_f8(a00, b0, t0);
-        t1 = mfma32_f8(a10, b0, t1);
-        t0 = mfma32_f8(a01, b1, t0);
-        t1 = mfma32_f8(a11, b1, t1);
-        promote(acc[0][j], t0, f);
-        promote(acc[1][j], t1, f);
+          for (int r = 0; r < 16; ++r) { t0[r] = 0.0f; t1[r] = 0.0f; }
+          t0 = mfma32_f8(a00, b0, t0);
+          t1 = mfma32_f8(a10, b0, t1);
+          t0 = mfma32_f8(a01, b1, t0);
+          t1 = mfma32_f8(a11, b1, t1);
+          promote(acc[0][j], t0, f);
+          promote(acc[1][j], t1, f);
+        }
       }
     }
   }
 
+  if (CH) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j < jlive) {
+        const int m = m0 + wm * 128 + j * 32 + fr;
+        if (m < M) {
+          const float sam = sa[m];
+          uint16_t* row = y + static_cast<int64_t>(m) * ldy;
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (n + r < N)
+                  row[n + r] = channel_out(acc[i][j][4 * q + r], sam, sw[n + r], bias ? bias[n + r] : 0.0f);
+            }
+        }
+      }
+    }
+    return;
+  }
   if (yp) {
     float* ypp = yp + static_cast<int64_t>(part) * M * N;
 #pragma unroll
@@ -235,19 +274,19 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 // The 128 KB of dynamic LDS is above the default limit: raise it once per device.
 constexpr int kMaxDevices = 64;
 
-std::once_flag g_lds_once[kMaxDevices][4];
-hipError_t g_lds_err[kMaxDevices][4];
+std::once_flag g_lds_once[kMaxDevices][8];
+hipError_t g_lds_err[kMaxDevices][8];
 
-template <bool HALF, bool GROUPED>
+template <bool HALF, bool GROUPED, bool CH = false>
 hipError_t ensure_lds_limit() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0);
+  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0);
   std::call_once(g_lds_once[dev][slot], [dev] {
     g_lds_err[dev][slot] = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED>),
+        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   });
   return g_lds_err[dev][slot];
@@ -266,6 +305,20 @@ hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t*
 }
 
 }  // namespace
+
+// Per-token / per-channel form: a.qa row-major [M][a.ldq], a.sa [M], a.sw [N]; any M.
+hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
+  if (static_cast<int64_t>(256) * a.ldq > int64_t{0xffffffff} || static_cast<int64_t>(256) * a.K > int64_t{0xffffffff})
+    return hipErrorInvalidValue;
+  hipError_t e = ensure_lds_limit<false, false, true>();
+  if (e != hipSuccess) return e;
+  const int mpad = (a.M + kBM - 1) / kBM * kBM;
+  const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (mpad / kBM));
+  gemm_prefill256_kernel<false, false, true><<<tiles, 512, kLdsBytes, stream>>>(
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, mpad, nullptr, nullptr, 0, 0, 0, 1, nullptr,
+      a.ldq);
+  return hipGetLastError();
+}
 
 // Requires K % 128 == 0, 16-byte aligned weights, Mpad % 256 == 0 (qa/sa
 // padded with zero rows up to Mpad).

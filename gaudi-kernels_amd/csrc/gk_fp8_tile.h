@@ -43,6 +43,19 @@ __device__ inline v4f mfma_f8(v8i a, v8i b) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, zero, 0, 0, 0, 0, 0, 0);
 }
 
+// Accumulating form (C = acc): the per-token / per-channel GEMM sums over all K
+// inside the matrix core (its scales do not vary along K).
+__device__ inline v4f mfma_f8_acc(v8i a, v8i b, v4f c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// Per-token / per-channel epilogue of the reference's channel finish
+// (csrc/tpc/block_fp8_framework/channel_finish.c:9-15): y = bf16(fma(p * sa[m],
+// sw[n], bias[n])) with the product p * sa rounded to fp32 first.
+__device__ inline uint16_t channel_out(float p, float sam, float swn, float bn) {
+  return bf16_rne(fmaf(mul_rn(p, sam), swn, bn));
+}
+
 // Writes C[n0 + 4*quad + r][m] (r = 0..3) of one 16x16 tile as bf16 with bias.
 __device__ inline void store_tile(uint16_t* __restrict__ y, int64_t ldy, const float* __restrict__ bias, int M,
                                   int N, int m, int n, v4f acc) {

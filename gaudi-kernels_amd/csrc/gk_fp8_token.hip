@@ -1,0 +1,126 @@
+// Per-token activation quantization and the per-channel epilogue of the
+// reference's per-token / per-channel W8A8 path, on gfx950.
+//
+// token quant (csrc/tpc/block_fp8_framework/activation_token.c:4-26, helpers
+// activation_quant_common.h:3-30): one scale per row,
+//   m     = max |x| over the row (1 where the row is all zero),
+//   s     = fp8_activation_scale(m) = fma(fma(-s0, 448, m), 1/448, s0), s0 = m * (1/448),
+//   z     = fma(fma(-q0, s, x), r, q0), q0 = x * r, r = 1/s   (the refined quotient),
+//   code  = E4M3 round-to-nearest-even of min(|z|, 448) with x's sign, then halved
+//           into the Gaudi2 half range (codec_half4: value / 2, RNE on its grid),
+//   scale = 2 s stored per row.
+// The reciprocal here is the IEEE one (the TPC reciprocal instruction's exact
+// rounding is not documented in the reference).  On gfx950 the encode is
+// v_cvt_pk_fp8_f32 (equal to the software RNE encoder for |v| <= 464).
+//
+// channel finish (channel_finish.c:2-18): y[r][c] = bf16(fma(p[r][c] * a[r], w[c], b[c])).
+
+#include "gk_fp8_tile.h"
+
+namespace gk {
+
+namespace {
+
+constexpr int kTokThreads = 256;
+
+__device__ inline float token_scale(float m) {  // activation_quant_common.h:3-7
+  const float inv448 = 1.0f / 448.0f;
+  const float s0 = mul_rn(m, inv448);
+  const float res = fmaf(-s0, 448.0f, m);
+  return fmaf(res, inv448, s0);
+}
+
+// 8 bf16 values -> 8 half-range codes (as two packed dwords).
+__device__ inline uint2 token_codes8(uint4 raw, float s, float r) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t out[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float z[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float x = bits_f32(h ? (w[i] & 0xffff0000u) : (w[i] << 16));
+      const float q0 = mul_rn(x, r);
+      const float zz = fmaf(fmaf(-q0, s, x), r, q0);
+      z[h] = copysignf(fminf(fabsf(zz), 448.0f), x);
+    }
+    const uint32_t two = __builtin_amdgcn_cvt_pk_fp8_f32(z[0], z[1], 0, false) & 0xffffu;
+    out[i >> 1] |= two << ((i & 1) * 16);
+  }
+  return make_uint2(codec_half4(out[0]), codec_half4(out[1]));
+}
+
+__global__ __launch_bounds__(kTokThreads) void token_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                  int width, uint8_t* __restrict__ q, int64_t ldq,
+                                                                  float* __restrict__ scales, int vec_ok) {
+  __shared__ float wmax[kTokThreads / 64];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* xr = x + static_cast<int64_t>(row) * ldx;
+  float m = 0.0f;
+  for (int c = tid * 8; c < width; c += kTokThreads * 8) {
+    if (vec_ok) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        m = fmaxf(m, fmaxf(fabsf(bits_f32(w[i] << 16)), fabsf(bits_f32(w[i] & 0xffff0000u))));
+    } else {
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(bf16_value(xr[c + j])));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((tid & 63) == 0) wmax[tid >> 6] = m;
+  __syncthreads();
+  m = wmax[0];
+#pragma unroll
+  for (int i = 1; i < kTokThreads / 64; ++i) m = fmaxf(m, wmax[i]);
+  if (m == 0.0f) m = 1.0f;  // only an all-zero token needs a substitute denominator (activation_token.c:16)
+  const float s = token_scale(m);
+  const float r = 1.0f / s;
+  uint8_t* qr = q + static_cast<int64_t>(row) * ldq;
+  for (int c = tid * 8; c < width; c += kTokThreads * 8) {
+    uint4 v;
+    if (vec_ok) {
+      v = *reinterpret_cast<const uint4*>(xr + c);
+    } else {
+      uint32_t h[8];
+      for (int j = 0; j < 8; ++j) h[j] = xr[c + j];
+      v = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    }
+    *reinterpret_cast<uint2*>(qr + c) = token_codes8(v, s, r);
+  }
+  if (tid == 0) scales[row] = 2.0f * s;
+}
+
+__global__ __launch_bounds__(256) void channel_finish_kernel(const float* __restrict__ p, int64_t ldp, int rows,
+                                                             int width, const float* __restrict__ a,
+                                                             const float* __restrict__ w, const float* __restrict__ b,
+                                                             uint16_t* __restrict__ y, int64_t ldy) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(rows) * width) return;
+  const int64_t r = i / width;
+  const int c = static_cast<int>(i - r * width);
+  y[r * ldy + c] = channel_out(p[r * ldp + c], a[r], w[c], b ? b[c] : 0.0f);
+}
+
+}  // namespace
+
+hipError_t launch_token_quant(const uint16_t* x, int64_t ldx, int rows, int width, uint8_t* q, int64_t ldq,
+                              float* scales, hipStream_t stream) {
+  const int vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && ldx % 8 == 0;
+  token_quant_kernel<<<rows, kTokThreads, 0, stream>>>(x, ldx, width, q, ldq, scales, vec_ok);
+  return hipGetLastError();
+}
+
+hipError_t launch_channel_finish(const float* partial, int64_t ldp, int rows, int width, const float* act_scales,
+                                 const float* w_scales, const float* bias, uint16_t* y, int64_t ldy,
+                                 hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(rows) * width;
+  channel_finish_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(partial, ldp, rows, width,
+                                                                                     act_scales, w_scales, bias, y,
+                                                                                     ldy);
+  return hipGetLastError();
+}
+
+}  // namespace gk

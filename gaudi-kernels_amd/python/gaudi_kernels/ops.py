@@ -365,3 +365,48 @@ def weights_finite(weight, scales):
     """True iff the E4M3FN weight holds no NaN code and its scales are finite and >= 0 (GPU check)."""
     x = torch.zeros((1, weight.shape[-1]), dtype=torch.bfloat16, device=weight.device)
     return inputs_finite(x, weight.reshape(-1, weight.shape[-1]), scales)
+
+
+def token_quant(x, *, out=None, scales=None):
+    """Per-token W8A8 activation quantization (gk_fp8_token_quant_bf16_v1) -> (half-range codes uint8
+    [rows, width], scales fp32 [rows] = 2 * max|x_row| / 448)."""
+    device = require_device(x.device)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("expected a 2-D bf16 activation with unit column stride")
+    rows, width = x.shape
+    q = torch.empty((rows, width), dtype=torch.uint8, device=device) if out is None else out
+    s = torch.empty(rows, dtype=torch.float32, device=device) if scales is None else scales
+    nat.check("gk_fp8_token_quant_bf16",
+              nat.load().gk_fp8_token_quant_bf16(_ptr(x), rows, width, x.stride(0), _ptr(q), q.stride(0), _ptr(s),
+                                                 _stream(device)))
+    return q, s
+
+
+def channel_finish(partial, act_scales, w_scales, bias=None, *, out=None):
+    """y = bf16(fma(partial * act_scales[:, None], w_scales, bias)) (gk_fp8_channel_finish_bf16_v1)."""
+    device = require_device(partial.device)
+    rows, width = partial.shape
+    y = torch.empty((rows, width), dtype=torch.bfloat16, device=device) if out is None else out
+    nat.check("gk_fp8_channel_finish_bf16",
+              nat.load().gk_fp8_channel_finish_bf16(_ptr(partial), rows, width, partial.stride(0), _ptr(act_scales),
+                                                    _ptr(w_scales), _ptr(bias), _ptr(y), y.stride(0),
+                                                    _stream(device)))
+    return y
+
+
+def channel_gemm(q, sa, weight, sw, bias=None, *, out=None):
+    """Per-token / per-channel W8A8 GEMM: codes q [M, K] with sa [M], weight codes [N, K] with sw [N] ->
+    bf16 [M, N] = bf16(fma(sum_k q w * sa, sw, bias))."""
+    device = require_device(q.device)
+    q8, w8 = _u8(q), _u8(weight)
+    m, k = q8.shape
+    n = w8.shape[0]
+    if w8.shape[1] != k or not w8.is_contiguous() or q8.stride(1) != 1:
+        raise ValueError("expected codes q [M, K] (unit column stride) and a contiguous weight [N, K]")
+    if sa.shape != (m,) or sw.shape != (n,) or (bias is not None and bias.shape != (n,)):
+        raise ValueError("expected sa [M], sw [N] and bias [N]")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=device) if out is None else out
+    nat.check("gk_fp8_channel_gemm_bf16",
+              nat.load().gk_fp8_channel_gemm_bf16(_ptr(q8), q8.stride(0), _ptr(sa), m, k, _ptr(w8), n, _ptr(sw),
+                                                  _ptr(bias), _ptr(y), y.stride(0), 0, _stream(device)))
+    return y

@@ -159,6 +159,39 @@ gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, 
                               const float* scales, int64_t n_scales, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* ---- per-token / per-channel W8A8 -------------------------------------------------- */
+
+/* The reference's gk_fp8_token_quant_bf16_v1 (csrc/tpc/block_fp8_framework/
+ * activation_token.c:4-26, glue generic_fp8_glue.hpp:31-50): x bf16 [rows,
+ * width] (width a multiple of 128, row stride ldx) -> q [rows, width]
+ * Gaudi2 half-range E4M3 codes (row stride ldq, a multiple of 8) and one fp32
+ * scale per row, scales[r] = 2 * s_r with s_r = max|x_r| / 448 (FMA-refined;
+ * 1 / 448 for an all-zero row).  Each code is the E4M3 round-to-nearest-even
+ * of min(|x / s_r|, 448), halved into the half range (codec rule). */
+gk_status gk_fp8_token_quant_bf16(const void* x, int64_t rows, int64_t width, int64_t ldx, void* q, int64_t ldq,
+                                  float* scales, void* stream);
+
+/* The reference's gk_fp8_channel_finish_bf16_v1 (channel_finish.c:2-18, glue
+ * generic_fp8_glue.hpp:52-82): fp32 partial [rows, width] (width a multiple
+ * of 128) -> y[r][c] = bf16(fma(partial[r][c] * act_scales[r], w_scales[c],
+ * bias[c])), the product rounded to fp32 first; bias may be NULL (zero). */
+gk_status gk_fp8_channel_finish_bf16(const float* partial, int64_t rows, int64_t width, int64_t ldp,
+                                     const float* act_scales, const float* w_scales, const float* bias, void* y,
+                                     int64_t ldy, void* stream);
+
+/* The per-token / per-channel GEMM: the MME product of the reference chain
+ * (token quant -> MME -> channel finish) fused with the channel finish.
+ * q: E4M3 codes [m, k] (row stride ldq, a multiple of 16; half-range codes
+ * from gk_fp8_token_quant_bf16 are read as the OCP codes of half their value,
+ * which the doubled scales restore), sa [m]; w: codes [n, k] (16-byte
+ * aligned, k a multiple of 128), sw [n] per output channel; bias [n] or NULL.
+ * y[i][j] = bf16(fma(P[i][j] * sa[i], sw[j], bias[j])), P the fp32 sum of the
+ * code products over k.  M <= 16 streams the weights; larger M runs the
+ * 256 x 256 MFMA kernel.  flags must be 0. */
+gk_status gk_fp8_channel_gemm_bf16(const void* q, int64_t ldq, const float* sa, int64_t m, int64_t k, const void* w,
+                                   int64_t n, const float* sw, const float* bias, void* y, int64_t ldy,
+                                   uint32_t flags, void* stream);
+
 /* ---- SiLU-and-mul ------------------------------------------------------------ */
 
 /* The reference's gk_silu_and_mul_bf16_v1 (csrc/tpc/generic_dense/
