@@ -8,7 +8,10 @@ E4M3 weights with fp32 128x128 block scales, bf16 activations quantized per
 1x128 group inside the op, bf16 output.  Inputs are synthetic (seeded
 N(0,0.02) weights with 5% x8 blocks, N(0,1) activations with 1% x20 outlier
 channels) and resident in HBM before timing starts.  Weight copies totalling
->= 512 MB are rotated so the 256 MB Infinity Cache cannot serve them.
+>= 512 MB are rotated so the 256 MB Infinity Cache cannot serve them.  The
+weights are in the load-time packed layout (ops.pack_weight, the same codes in
+matrix-instruction fragment order; results bit-identical to row-major
+weights); the row-major kernel times are reported beside them.
 
 value = algorithmic bytes of the sweep / time per sweep (GB/s), with bytes per
 GEMM B = N*K + 4*ceil(N/128)*ceil(K/128) + 2*M*K + 2*M*N.  Side measurements
@@ -35,6 +38,8 @@ METRIC = "block-FP8 GEMM GB/s & TFLOP/s (% roofline) at M=1..16 and M=4096"
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5033.0   # dense, 256 CU x 8192 FLOP/clk x 2.4 GHz
 MALL_ROTATE_BYTES = 512 << 20
+# The dominant kernel: the decode GEMM instance config 2 runs on packed weights (NW=8, R=2, U=4, QPACK, WPACK).
+DECODE_KERNEL = "gk::gemm_decode_kernel<8,2,4,false,true,false,true>"
 
 
 def gemm_bytes(m, n, k, bias=False):
@@ -51,12 +56,19 @@ def log(msg):
 
 
 class Rotation:
-    """Distinct device copies of one weight/scale pair totalling >= MALL_ROTATE_BYTES."""
+    """Distinct device copies of one weight/scale pair totalling >= MALL_ROTATE_BYTES.
 
-    def __init__(self, w, s, min_bytes=MALL_ROTATE_BYTES):
+    packed=True: each copy is the load-time packed layout (ops.pack_weight) of the weight.
+    """
+
+    def __init__(self, w, s, min_bytes=MALL_ROTATE_BYTES, packed=False):
         copies = max(1, -(-min_bytes // (w.numel() + 4 * s.numel())))
         wd, sd = w.cuda(), s.cuda()
-        self.items = [(wd, sd)] + [(wd.clone(), sd.clone()) for _ in range(copies - 1)]
+        if packed:
+            from gaudi_kernels import ops
+            self.items = [(ops.pack_weight(wd), sd if i == 0 else sd.clone()) for i in range(copies)]
+        else:
+            self.items = [(wd, sd)] + [(wd.clone(), sd.clone()) for _ in range(copies - 1)]
         self.i = 0
 
     def next(self):
@@ -219,7 +231,8 @@ def main():
     n, k = 6144, 4096
     ms_list = (1, 2, 4, 8, 16)
     w, s = synth.weight(n, k, seed=2000)
-    rot = Rotation(w, s)
+    rot = Rotation(w, s, packed=True)
+    rot_row = Rotation(w, s)
     xs = {m: synth.activations(m, k, seed=2001 + m).cuda() for m in ms_list}
     outs = {m: torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for m in ms_list}
     wss = {m: ops.make_workspace(m, n, k) for m in ms_list}
@@ -261,16 +274,20 @@ def main():
         q, sa = ops.act_quant(xs[m], decode_layout=True)
         kern_ms = time_loop(lambda: ops.block_fp8_gemm_q(q, sa, m, *rot.next(), out=outs[m], decode_layout=True),
                             100, 10)
+        row_ms = time_loop(lambda: ops.block_fp8_gemm_q(q, sa, m, *rot_row.next(), out=outs[m], decode_layout=True),
+                           100, 10)
         b = gemm_bytes(m, n, k)
         per_m[str(m)] = {"op_us": round(op_ms * 1e3, 2), "op_GBps": round(b / (op_ms * 1e-3) / 1e9, 1),
                          "gemm_kernel_us": round(kern_ms * 1e3, 2),
                          "gemm_kernel_GBps": round(b / (kern_ms * 1e-3) / 1e9, 1),
-                         "gemm_kernel_hbm_frac": round(b / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                         "gemm_kernel_hbm_frac": round(b / (kern_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                         "gemm_kernel_rowmajor_us": round(row_ms * 1e3, 2)}
         if m == 16:
             kernel_us_m16 = kern_ms * 1e3
         log(f"[bench]   M={m}: op {op_ms * 1e3:.2f} us ({per_m[str(m)]['op_GBps']} GB/s), "
-            f"gemm kernel {kern_ms * 1e3:.2f} us ({per_m[str(m)]['gemm_kernel_GBps']} GB/s)")
-    del rot
+            f"gemm kernel {kern_ms * 1e3:.2f} us ({per_m[str(m)]['gemm_kernel_GBps']} GB/s), "
+            f"row-major weights {row_ms * 1e3:.2f} us")
+    del rot, rot_row
     torch.cuda.empty_cache()
 
     # Plain device-to-device copy of a known size: the calibration kernel for
@@ -288,9 +305,9 @@ def main():
     achieved = b16 / (kernel_us_m16 * 1e-6) / 1e9
     result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(achieved / PEAK_HBM_GBS, 4),
-                          "traffic": measured_traffic("gk::gemm_decode_kernel", "config2"),
+                          "traffic": measured_traffic(DECODE_KERNEL, "config2"),
                           "traffic_source": "profiles/block_fp8_gemm_bench.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
-                          "kernel": "gk::gemm_decode_kernel (M=16, N=6144, K=4096)",
+                          "kernel": f"{DECODE_KERNEL} (M=16, N=6144, K=4096, packed weights)",
                           "bytes_per_launch": b16, "avg_launch_us": round(kernel_us_m16, 3)}
     result["decode_sweep"] = per_m
 
@@ -300,19 +317,23 @@ def main():
         pair = []
         for (nn, kk, seed) in ((28672, 4096, 3000), (4096, 14336, 3100)):
             w3, s3 = synth.weight(nn, kk, seed=seed)
-            r3 = Rotation(w3, s3)
             x3 = synth.activations(m, kk, seed=seed + 1).cuda()
             o3 = torch.empty((m, nn), dtype=torch.bfloat16, device="cuda")
             ws3 = ops.make_workspace(m, nn, kk)
-            ms3 = time_loop(lambda: ops.block_fp8_gemm(x3, *r3.next(), out=o3, workspace=ws3), 30, 5)
-            pair.append((nn, kk, ms3))
-            del r3
-            torch.cuda.empty_cache()
-        tb = sum(gemm_bytes(m, nn, kk) for nn, kk, _ in pair)
-        tt = sum(t for _, _, t in pair)
+            times = []
+            for packed in (True, False):
+                r3 = Rotation(w3, s3, packed=packed)
+                times.append(time_loop(lambda: ops.block_fp8_gemm(x3, *r3.next(), out=o3, workspace=ws3), 30, 5))
+                del r3
+                torch.cuda.empty_cache()
+            pair.append((nn, kk, times[0], times[1]))
+        tb = sum(gemm_bytes(m, nn, kk) for nn, kk, _, _ in pair)
+        tt = sum(t for _, _, t, _ in pair)
         result["mlp_pair_m16"] = {"us": round(tt * 1e3, 2), "GBps": round(tb / (tt * 1e-3) / 1e9, 1),
                                   "hbm_frac": round(tb / (tt * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                                  "gate_up_us": round(pair[0][2] * 1e3, 2), "down_us": round(pair[1][2] * 1e3, 2)}
+                                  "gate_up_us": round(pair[0][2] * 1e3, 2), "down_us": round(pair[1][2] * 1e3, 2),
+                                  "rowmajor_gate_up_us": round(pair[0][3] * 1e3, 2),
+                                  "rowmajor_down_us": round(pair[1][3] * 1e3, 2)}
         log(f"[bench] mlp pair: {result['mlp_pair_m16']}")
 
     # ---- config 4: prefill ------------------------------------------------------------------------
@@ -321,17 +342,20 @@ def main():
         w4, s4 = synth.weight(nn, kk, seed=4000)
         x4 = synth.activations(m, kk, seed=4001).cuda()
         w4d, s4d = w4.cuda(), s4.cuda()
+        p4 = ops.pack_weight(w4d)
         o4 = torch.empty((m, nn), dtype=torch.bfloat16, device="cuda")
         ws4 = ops.make_workspace(m, nn, kk)
-        ms4 = time_loop(lambda: ops.block_fp8_gemm(x4, w4d, s4d, out=o4, workspace=ws4), 20, 3)
+        ms4 = time_loop(lambda: ops.block_fp8_gemm(x4, p4, s4d, out=o4, workspace=ws4), 20, 3)
         _, m_pad, _ = ops.plan(m, nn, kk)
         q4, sa4 = ops.act_quant(x4, m_pad=m_pad)
-        ms4k = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, w4d, s4d, out=o4), 20, 3)
+        ms4k = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, p4, s4d, out=o4), 20, 3)
+        ms4r = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, w4d, s4d, out=o4), 20, 3)
         f = gemm_flops(m, nn, kk)
         result["prefill_m4096"] = {"op_us": round(ms4 * 1e3, 1), "gemm_kernel_us": round(ms4k * 1e3, 1),
                                    "op_TFLOPs": round(f / (ms4 * 1e-3) / 1e12, 1),
                                    "gemm_kernel_TFLOPs": round(f / (ms4k * 1e-3) / 1e12, 1),
-                                   "gemm_kernel_mfma_frac": round(f / (ms4k * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+                                   "gemm_kernel_mfma_frac": round(f / (ms4k * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+                                   "gemm_kernel_rowmajor_us": round(ms4r * 1e3, 1)}
         log(f"[bench] prefill: {result['prefill_m4096']}")
 
     # ---- config 5: MoE layer ----------------------------------------------------------------------
@@ -392,7 +416,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp8e4m3", "data": "synthetic",
         "config": {"workload": "config2 QKV decode sweep: block-FP8 GEMM at M=1,2,4,8,16, N=6144, K=4096, "
-                               "128x128 fp32 weight scales, 1x128 activation groups, bf16 out",
+                               "128x128 fp32 weight scales, 1x128 activation groups, bf16 out; weights in the "
+                               "load-time packed layout",
                    "sweep_bytes": sweep_bytes, "sweep_flops": sweep_flops, "device": dev_name},
         **result,
         "cpu_baseline": cpu,

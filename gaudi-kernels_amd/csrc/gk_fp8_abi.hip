@@ -15,6 +15,8 @@
 #include <mutex>
 
 #include "../../include/gk_fp8.h"
+#include <algorithm>
+
 #include "gk_fp8_internal.h"
 
 namespace {
@@ -33,11 +35,12 @@ constexpr const char* kOps[] = {
     "gk_fp8_silu_mul_quant_bf16_v1",  // SiLU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
     "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (build-defined)
+    "gk_fp8_pack_weight_v1",        // load-time layout packing (fp8_codec.py:19 "a separate step")
 };
 constexpr uint32_t kNumOps = sizeof(kOps) / sizeof(kOps[0]);
 
-constexpr uint32_t kKnownFlags =
-    GK_FLAG_NATIVE_HALF | GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL | GK_FLAG_FORCE_GENERIC;
+constexpr uint32_t kKnownFlags = GK_FLAG_NATIVE_HALF | GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL |
+                                  GK_FLAG_FORCE_GENERIC | GK_FLAG_WEIGHT_PACKED;
 constexpr size_t kStatusBytes = 256;
 constexpr int64_t kMaxDim = (int64_t{1} << 31) - 1;
 
@@ -106,7 +109,7 @@ struct Plan {
   int variant;
   int64_t m_pad;
   size_t q_bytes = 0, sa_bytes = 0;  // quantized activations [G][m_pad][128] and scales [G][m_pad]
-  gk::DecodeShape dec{0, 0};
+  gk::DecodeShape dec{0, 0, 0};
 };
 
 gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, Plan* p) {
@@ -115,6 +118,8 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
   const uint32_t force = flags & (GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL | GK_FLAG_FORCE_GENERIC);
   if (force & (force - 1)) return GK_UNSUPPORTED_LAYER_CONFIGURATION;  // more than one forced variant
   const bool tiled_ok = (k % 128 == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
+  const bool wpack = (flags & GK_FLAG_WEIGHT_PACKED) != 0;
+  if (wpack && (!tiled_ok || force == GK_FLAG_FORCE_GENERIC)) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
   const int64_t g = (k + 127) / 128;
   int variant;
   if (force == GK_FLAG_FORCE_GENERIC || (!force && !tiled_ok)) {
@@ -136,8 +141,23 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
                                              : m;
   p->q_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 128);
   p->sa_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 4);
-  if (variant == GK_VARIANT_DECODE) p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g));
+  if (variant == GK_VARIANT_DECODE) p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g), wpack);
+  // Packed weights at M > 16 run the 256 x 256 kernel, which addresses its panels with 32-bit offsets.
+  if (wpack && variant == GK_VARIANT_PREFILL && (p->m_pad * g * 128 > int64_t{0xffffffff} || 256 * k > int64_t{0xffffffff}))
+    return GK_UNSUPPORTED_LAYER_CONFIGURATION;
   return GK_SUCCESS;
+}
+
+// Decode GEMM with the quantizer fused: every workgroup quantizes the
+// ceil(M/4) token rows of 4 it needs over its K range.  That redundant work,
+// relative to one workgroup per CU over K = 4096 with all 16 rows, is
+// (workgroups / 256) * (K / 4096) * ceil(M/4) / 4; measured on MI355X, fusing
+// beats the separate quantizer launch while it stays <= 0.4 (config 2 at
+// M <= 8; never the 28672 x 4096 or 4096 x 14336 shapes).
+bool fused_quant_pays(int64_t m, int64_t n, int64_t k, const gk::DecodeShape& d) {
+  const double wgs = static_cast<double>((n + 16 * d.r - 1) / (16 * d.r));
+  const double rows4 = static_cast<double>((std::min<int64_t>(m, 16) + 3) / 4);
+  return (wgs / 256.0) * (static_cast<double>(k) / 4096.0) * (rows4 / 4.0) <= 0.4;
 }
 
 gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* scales, int64_t scale_rows,
@@ -150,9 +170,10 @@ gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* sc
   return GK_SUCCESS;
 }
 
+// xq_ldx > 0: q is the bf16 activation x (row stride xq_ldx elements), quantized inside the decode kernel.
 gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, int64_t k, const void* w,
                    int64_t n, const float* scales, const float* bias, void* y, int64_t ldy, uint32_t flags,
-                   bool qpack, hipStream_t stream) {
+                   bool qpack, hipStream_t stream, int64_t xq_ldx = 0) {
   gk::GemmArgs a;
   a.qa = q;
   a.sa = sa;
@@ -169,6 +190,9 @@ gk_status run_gemm(const Plan& p, const uint8_t* q, const float* sa, int64_t m, 
   a.half_w = (flags & GK_FLAG_NATIVE_HALF) != 0;
   a.dec = p.dec;
   a.qpack = qpack;
+  a.wpack = (flags & GK_FLAG_WEIGHT_PACKED) != 0;
+  a.xq = xq_ldx > 0;
+  a.ldq = xq_ldx;
   hipError_t e;
   switch (p.variant) {
     case GK_VARIANT_DECODE: e = gk::launch_gemm_decode(a, stream); break;
@@ -272,6 +296,26 @@ gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx
                                        (flags & GK_FLAG_NATIVE_HALF) != 0, packed, static_cast<hipStream_t>(stream)));
 }
 
+gk_status gk_fp8_packed_weight_bytes(int64_t n, int64_t k, size_t* bytes) {
+  if (!bytes) return GK_INVALID_ARGUMENT;
+  if (n < 1 || k < 128 || k % 128 != 0 || n > kMaxDim || k > kMaxDim) return GK_INCOMPATIBLE_INPUT_SIZE;
+  *bytes = static_cast<size_t>(gk::packed_weight_bytes(n, k));
+  return GK_SUCCESS;
+}
+
+gk_status gk_fp8_pack_weight(const void* w, int64_t n, int64_t k, void* packed, size_t packed_bytes, void* stream) {
+  if (!w || !packed) return GK_INVALID_ARGUMENT;
+  size_t need = 0;
+  gk_status st = gk_fp8_packed_weight_bytes(n, k, &need);
+  if (st != GK_SUCCESS) return st;
+  if (packed_bytes < need) return GK_INSUFFICIENT_BUFFER;
+  if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(packed)) & 15) return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_pack_weight(static_cast<const uint8_t*>(w), static_cast<int>(n), static_cast<int>(k),
+                                         static_cast<uint8_t*>(packed), static_cast<hipStream_t>(stream)));
+}
+
 gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, int* variant,
                                  int64_t* m_pad, size_t* workspace_bytes) {
   Plan p;
@@ -300,6 +344,13 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
   st = current_device_ok();
   if (st != GK_SUCCESS) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Decode variant with 16-byte aligned activation rows and little redundant
+  // quantization work: the GEMM quantizes x itself (one launch, the same
+  // codes and scales as the quantizer below).
+  if (p.variant == GK_VARIANT_DECODE && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 8 == 0 &&
+      fused_quant_pays(m, n, k, p.dec))
+    return run_gemm(p, static_cast<const uint8_t*>(x), nullptr, m, k, w, n, scales, bias, y, ldy, flags, false, s,
+                    ldx);
   uint8_t* q = static_cast<uint8_t*>(workspace);
   float* sa = reinterpret_cast<float*>(q + p.q_bytes);
   // The decode variant takes its activations in the packed fragment layout.

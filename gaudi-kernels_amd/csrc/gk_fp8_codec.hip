@@ -178,6 +178,26 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   }
 }
 
+// ---- load-time weight packing (fragment order of the FP8 matrix instructions) ----
+// One thread per 16-byte piece o of the output: block b = o / 128 = (tile t,
+// group g), piece (h, l) = ((o / 64) % 2, o % 64) <- bytes [128 g + 32 (l/16)
+// + 16 h, +16) of row 16 t + l%16; rows >= N give zeros.  The writes are
+// contiguous; each wave's reads cover 16 rows x 64 bytes.
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint8_t* __restrict__ w, int N, int K, int G,
+                                                          uint8_t* __restrict__ out, int64_t pieces) {
+  for (int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; o < pieces;
+       o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t b = o >> 7;
+    const int h = static_cast<int>((o >> 6) & 1), l = static_cast<int>(o & 63);
+    const int t = static_cast<int>(b / G), g = static_cast<int>(b - static_cast<int64_t>(t) * G);
+    const int row = 16 * t + (l & 15);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < N)
+      v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(row) * K + 128 * g + 32 * (l >> 4) + 16 * h);
+    *reinterpret_cast<uint4*>(out + o * 16) = v;
+  }
+}
+
 // ---- launchers -----------------------------------------------------------------
 static int codec_grid(int64_t nvec) {
   int64_t blocks = (nvec + 255) / 256;
@@ -214,6 +234,13 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
     e = hipGetLastError();
   }
   return e;
+}
+
+hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, hipStream_t stream) {
+  if (N < 1 || K < 128 || K % 128 != 0) return hipErrorInvalidValue;
+  const int64_t pieces = packed_weight_bytes(N, K) / 16;
+  pack_weight_kernel<<<codec_grid(pieces), 256, 0, stream>>>(w, N, K, K / 128, packed, pieces);
+  return hipGetLastError();
 }
 
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,

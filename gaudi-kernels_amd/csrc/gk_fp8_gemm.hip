@@ -55,11 +55,28 @@ namespace gk {
 // clamped) and all loads of a step are issued before the first use: the
 // compiler then waits on them one by one instead of draining the queue.
 //
+// WPACK: weights in the fragment-packed layout (launch_pack_weight): lane l
+// of a tile's group reads pieces (0, l) and (1, l), two contiguous 1 KB loads
+// per wave that land in the MFMA layout directly -- no LDS transpose.  The
+// operands, and so the results, are bit-identical to the row-major path.
+//
+// XQ: the activations come as bf16 x [M][ldq] and are quantized inside the
+// kernel by the standalone quantizer's own code (quant_group8): per group,
+// load j (of 4) gives 16 lanes to each of tokens 4j..4j+3, 8 elements a lane
+// (full 128-byte lines), and the codes go through a wave-private LDS buffer
+// into the fragment layout.  The x loads of a step are issued before its
+// weight loads, so the quantizer's arithmetic overlaps the weight fetch
+// instead of costing a separate launch and memory round trip.  Every
+// workgroup quantizes the activations of its K range again, so this pays
+// only while that work is small (few tokens, few workgroups; the caller
+// decides).  Codes and scales are the standalone quantizer's, so the results
+// equal quantize-then-GEMM bit for bit.
+//
 // CH (per-token / per-channel scaling): activations row-major [M][ldq], one
 // scale per token sa[m] and per output channel sw[n]; the MFMAs accumulate
 // over all of K (no per-group promotion) and the epilogue applies
 // bf16(fma(p * sa[m], sw[n], bias[n])) (channel_finish.c:9-15).
-template <int NW, int R, int U, bool HALF, bool QPACK, bool CH = false>
+template <int NW, int R, int U, bool HALF, bool QPACK, bool CH = false, bool WPACK = false, bool XQ = false>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -68,7 +85,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
                                                               uint16_t* __restrict__ y, int64_t ldy, int M,
                                                               int N, int K, int G, int64_t ldq = 0) {
   static_assert(16 * R <= 128 && NW >= R, "a workgroup's rows lie in one 128-row scale block");
-  __shared__ __attribute__((aligned(16))) uint8_t tile[NW][2048];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[WPACK ? 1 : NW][2048];
+  __shared__ __attribute__((aligned(16))) uint8_t xqbuf[XQ ? NW : 1][XQ ? U : 1][2048 + 64];  // codes + 16 scales
   __shared__ v4f red[NW][R][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -76,13 +94,20 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   const int n0 = blockIdx.x * 16 * R;
   const int lrow = 2 * (lane >> 4) + ((lane >> 3) & 1), lch = lane & 7;
   const uint8_t* wp[R];
-  int64_t d8[R];  // byte distance from row lrow to row lrow + 8 (rows past N re-read row N-1)
+  int64_t d8[R];  // row-major: byte distance from row lrow to row lrow + 8 (rows past N re-read row N-1)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int a0 = min(n0 + 16 * r + lrow, N - 1), a1 = min(n0 + 16 * r + lrow + 8, N - 1);
-    wp[r] = w + static_cast<int64_t>(a0) * K + lch * 16;
-    d8[r] = static_cast<int64_t>(a1 - a0) * K;
+    if (WPACK) {  // tiles past the last re-read the last tile (never stored)
+      const int t = min((n0 >> 4) + r, ((N + 15) >> 4) - 1);
+      wp[r] = w + static_cast<int64_t>(t) * G * 2048 + lane * 16;
+      d8[r] = 1024;
+    } else {
+      const int a0 = min(n0 + 16 * r + lrow, N - 1), a1 = min(n0 + 16 * r + lrow + 8, N - 1);
+      wp[r] = w + static_cast<int64_t>(a0) * K + lch * 16;
+      d8[r] = static_cast<int64_t>(a1 - a0) * K;
+    }
   }
+  constexpr int kWG = WPACK ? 2048 : 128;  // weight bytes from one group to the next
   const uint32_t woff0 = lrow * 128 + ((lch ^ ((lrow >> 1) & 7)) << 4);
   const uint32_t woff1 = (lrow + 8) * 128 + ((lch ^ (((lrow + 8) >> 1) & 7)) << 4);
   const uint32_t roff0 = col * 128 + (((2 * quad) ^ ((col >> 1) & 7)) << 4);
@@ -91,49 +116,99 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   const uint8_t* qp = CH      ? qa + tok * ldq + quad * 32
                       : QPACK ? qa + (16 * quad + tok) * 16
                               : qa + tok * 128 + quad * 32;
+  // XQ loader: load j reads token 4j + lane/16 (tokens >= M re-read token
+  // M-1), elements [8 (lane%16), +8) of the group; its 8 codes are bytes
+  // e0 = 8 (lane%16) .. e0+7 of that token, which the fragment layout keeps
+  // in piece (h, L) = ((e0/16) & 1, 16 (e0/32) + token) at byte e0 % 16.
+  const uint8_t* xrow[4];
+  uint32_t xwoff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = 4 * j + (lane >> 4), e0 = 8 * (lane & 15);
+    xrow[j] = qa + (static_cast<int64_t>(min(t, M - 1)) * ldq + e0) * 2;
+    xwoff[j] = ((e0 >> 4) & 1) * 1024 + 16 * (16 * (e0 >> 5) + t) + (e0 & 15);
+  }
+  // Token rows 4j..4j+3 with 4j >= M are neither loaded nor quantized: their
+  // fragment columns hold whatever the buffer held and are never stored.
+  const int xjn = (min(M, 16) + 3) >> 2;
   constexpr int kQHi = QPACK ? 1024 : 16;
   constexpr int kQG = CH ? 128 : 2048;              // bytes from one group to the next
-  const float* sap = sa + tok;                      // + g * 16
+  const float* sap = XQ ? sa : sa + tok;            // + g * 16 (unused with XQ)
   const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
-  uint8_t* buf = tile[wave];
+  uint8_t* buf = tile[WPACK ? 0 : wave];
 
   v4f acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   for (int g0 = gbeg; g0 < gend; g0 += U) {
-    uint4 wa[U][R][2], qb[U][2];
+    uint4 wa[U][R][2], qb[U][2], xb[XQ ? U : 1][4];
     float sv[U], wv[U];
+    if (XQ) {  // activations first: they are needed before the weights
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t go = static_cast<int64_t>(min(g0 + u, gend - 1)) * 256;  // 128 bf16
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j < xjn) xb[u][j] = *reinterpret_cast<const uint4*>(xrow[j] + go);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = min(g0 + u, gend - 1);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint8_t* p = wp[r] + static_cast<int64_t>(g) * 128;
+        const uint8_t* p = wp[r] + static_cast<int64_t>(g) * kWG;
         wa[u][r][0] = load_stream16(p);
         wa[u][r][1] = load_stream16(p + d8[r]);
       }
-      const uint8_t* q = qp + static_cast<int64_t>(g) * kQG;
-      qb[u][0] = *reinterpret_cast<const uint4*>(q);
-      qb[u][1] = *reinterpret_cast<const uint4*>(q + kQHi);
+      if (!XQ) {
+        const uint8_t* q = qp + static_cast<int64_t>(g) * kQG;
+        qb[u][0] = *reinterpret_cast<const uint4*>(q);
+        qb[u][1] = *reinterpret_cast<const uint4*>(q + kQHi);
+      }
       if (!CH) {
-        sv[u] = sap[g * 16];
+        if (!XQ) sv[u] = sap[g * 16];
         wv[u] = swp[g];
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the step is in flight before the first use
+    v8i bq[XQ ? U : 1];
+    if (XQ) {
+      uint8_t* xq = xqbuf[wave][0];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (j >= xjn) continue;  // wave-uniform: token rows 4j.. are all >= M
+          float sc;
+          const uint2 c = quant_group8(xb[u][j], true, HALF, &sc);
+          *reinterpret_cast<uint2*>(xq + u * (2048 + 64) + xwoff[j]) = c;
+          if ((lane & 15) == 0) *reinterpret_cast<float*>(xq + u * (2048 + 64) + 2048 + 4 * (4 * j + (lane >> 4))) = sc;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {  // same wave: its LDS accesses complete in order
+        const uint8_t* b = xq + u * (2048 + 64);
+        bq[u] = pack8(*reinterpret_cast<const uint4*>(b + 16 * lane), *reinterpret_cast<const uint4*>(b + 1024 + 16 * lane));
+        sv[u] = *reinterpret_cast<const float*>(b + 2048 + 4 * col);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const v8i b = pack8(qb[u][0], qb[u][1]);
+      const v8i b = XQ ? bq[u] : pack8(qb[u][0], qb[u][1]);
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
       const float f = CH ? 0.0f : (g0 + u < gend) ? sv[u] * (HALF ? 2.0f * wv[u] : wv[u]) : 0.0f;
       const bool live = g0 + u < gend;  // the clamped repeat of the last group adds nothing
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        *reinterpret_cast<uint4*>(buf + woff0) = wa[u][r][0];
-        *reinterpret_cast<uint4*>(buf + woff1) = wa[u][r][1];
-        const uint4 lo = *reinterpret_cast<const uint4*>(buf + roff0);
-        const uint4 hi = *reinterpret_cast<const uint4*>(buf + roff1);
+        uint4 lo = wa[u][r][0], hi = wa[u][r][1];
+        if (!WPACK) {
+          *reinterpret_cast<uint4*>(buf + woff0) = wa[u][r][0];
+          *reinterpret_cast<uint4*>(buf + woff1) = wa[u][r][1];
+          lo = *reinterpret_cast<const uint4*>(buf + roff0);
+          hi = *reinterpret_cast<const uint4*>(buf + roff1);
+        }
         if (CH) {
           if (live) acc[r] = mfma_f8_acc(weight_frag<HALF>(lo, hi), b, acc[r]);
         } else {
@@ -319,29 +394,41 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __rest
 template <int NW, int R, int U>
 static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
-#define GK_DECODE_LAUNCH(H, P)                                                                               \
-  gemm_decode_kernel<NW, R, U, H, P><<<grid, NW * 64, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, \
-                                                                   a.M, a.N, a.K, a.G)
+#define GK_DECODE_LAUNCH(H, P, WP, X)                                                                          \
+  gemm_decode_kernel<NW, R, U, H, P, false, WP, X><<<grid, NW * 64, 0, stream>>>(                               \
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq)
+#define GK_DECODE_LAUNCH_P(H, P, X) \
+  if (a.wpack) GK_DECODE_LAUNCH(H, P, true, X); else GK_DECODE_LAUNCH(H, P, false, X)
+#define GK_DECODE_LAUNCH_A(H)                         \
+  if (a.xq) { GK_DECODE_LAUNCH_P(H, false, true); }      \
+  else if (a.qpack) { GK_DECODE_LAUNCH_P(H, true, false); } \
+  else { GK_DECODE_LAUNCH_P(H, false, false); }
   if (a.half_w) {
-    if (a.qpack) GK_DECODE_LAUNCH(true, true); else GK_DECODE_LAUNCH(true, false);
+    GK_DECODE_LAUNCH_A(true)
   } else {
-    if (a.qpack) GK_DECODE_LAUNCH(false, true); else GK_DECODE_LAUNCH(false, false);
+    GK_DECODE_LAUNCH_A(false)
   }
+#undef GK_DECODE_LAUNCH_A
+#undef GK_DECODE_LAUNCH_P
 #undef GK_DECODE_LAUNCH
   return hipGetLastError();
 }
 
-DecodeShape plan_decode_shape(int N, int G) {
-  // R: 16-row tiles per workgroup.  Activation fragments are loaded once per
-  // group for R weight tiles, so larger R cuts activation traffic, but the
-  // workgroup count (tiles / R) must stay near or above the 256 CUs.
-  // NW: waves splitting K; measured on MI355X (M = 16): N=6144/K=4096 best at
-  // (R, NW) = (2, 8), N=28672/K=4096 at (4, 4), N=4096/K=14336 at (1, 16).
+DecodeShape plan_decode_shape(int N, int G, bool packed_weights) {
+  // R: 16-row tiles per workgroup.  Every workgroup reads the activations of
+  // its K range once, so larger R cuts activation traffic, but the workgroup
+  // count (tiles / R) must stay near or above the 256 CUs.  NW: waves
+  // splitting K (the partials are summed in wave order, so NW fixes the
+  // result bits; both weight layouts use the same NW for every N and give
+  // identical results).  U: groups per load step.  Measured on MI355X at
+  // M = 16 for N x K = 28672 x 4096, 6144 x 4096, 4096 x 14336; the packed
+  // layout (no LDS transpose) gains from the deeper step at N = 6144.
   (void)G;
   const int tiles = (N + 15) / 16;
-  if (tiles >= 1536) return DecodeShape{4, 4};
-  if (tiles >= 384) return DecodeShape{8, 2};
-  return DecodeShape{16, 1};
+  if (tiles >= 1536) return DecodeShape{2, 2, 4};
+  if (tiles >= 384) return packed_weights ? DecodeShape{8, 2, 4} : DecodeShape{8, 2, 2};
+  if (tiles >= 256) return DecodeShape{8, 1, 2};
+  return DecodeShape{16, 1, 2};
 }
 
 template <int NW, int R, int U>
@@ -352,12 +439,16 @@ static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Instantiated decode shapes (NW, R, U); plan_decode_shape returns only these.
+#define GK_DECODE_SHAPES(X) X(2, 2, 4) X(8, 2, 2) X(8, 2, 4) X(8, 1, 2) X(16, 1, 2)
+
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
-  const int key = a.dec.nw * 10 + a.dec.r;
+  const int key = a.dec.nw * 100 + a.dec.r * 10 + a.dec.u;
   switch (key) {
-    case 44: return decode_launch<4, 4, 4>(a, stream);
-    case 82: return decode_launch<8, 2, 2>(a, stream);
-    case 161: return decode_launch<16, 1, 2>(a, stream);
+#define GK_CASE(NW, R, U) \
+  case NW * 100 + R * 10 + U: return decode_launch<NW, R, U>(a, stream);
+    GK_DECODE_SHAPES(GK_CASE)
+#undef GK_CASE
     default: return hipErrorInvalidValue;
   }
 }
@@ -365,7 +456,8 @@ hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
   // M > 128: 256 x 256 tiles (gk_fp8_prefill.hip); smaller M wastes less on 128 x 128 tiles.
   // The 256 kernel addresses each operand panel with 32-bit offsets.
-  if (a.M > 128 && prefill256_fits(a)) return launch_gemm_prefill256(a, stream);
+  if ((a.M > 128 || a.wpack) && prefill256_fits(a)) return launch_gemm_prefill256(a, stream);
+  if (a.wpack) return hipErrorInvalidValue;  // packed weights: 256 x 256 kernel only
   const dim3 grid((a.N + kPB - 1) / kPB, (a.M + kPB - 1) / kPB);
   if (a.half_w)
     gemm_prefill_kernel<true><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,
@@ -378,11 +470,12 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
 
 hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream) {
   if (a.M > kDecodeMaxRows) return launch_gemm_channel256(a, stream);
-  const DecodeShape d = plan_decode_shape(a.N, a.G);
-  switch (d.nw * 10 + d.r) {
-    case 44: return decode_channel_launch<4, 4, 4>(a, stream);
-    case 82: return decode_channel_launch<8, 2, 2>(a, stream);
-    case 161: return decode_channel_launch<16, 1, 2>(a, stream);
+  const DecodeShape d = plan_decode_shape(a.N, a.G, false);
+  switch (d.nw * 100 + d.r * 10 + d.u) {
+#define GK_CASE(NW, R, U) \
+  case NW * 100 + R * 10 + U: return decode_channel_launch<NW, R, U>(a, stream);
+    GK_DECODE_SHAPES(GK_CASE)
+#undef GK_CASE
     default: return hipErrorInvalidValue;
   }
 }

@@ -17,11 +17,27 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kDecodeMaxRows = 16;   // decode variant: M <= 16, padded to one MFMA column tile
 constexpr int kPrefillRowTile = 256; // prefill variant: M padded to the token tile
 
+// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in VALU
+// data-parallel moves: xor 1 and xor 2 (quad_perm), then the half-row and
+// row mirrors pair quads 0-1 / 2-3 and the two halves.  Lanes whose source is
+// inactive keep their own value.  The maximum does not depend on the order.
+template <int CTRL>
+__device__ inline float dpp_fmax(float v) {
+  const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false);
+  return fmaxf(v, __int_as_float(o));
+}
+__device__ inline float row_max16(float v) {
+  v = dpp_fmax<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_fmax<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_fmax<0x141>(v);  // row_half_mirror
+  return dpp_fmax<0x140>(v);  // row_mirror
+}
+
 // ---- 1x128 activation quantizer (block_fp8_oracle.py:25-28, :32,:34) -------
 // Sixteen consecutive lanes own one 128-element group, 8 bf16 each (one
 // 16-byte load).  Returns the lane's 8 OCP E4M3 codes (byte i = element i)
 // and writes the group's scale (x2 in native_half mode).  amax is reduced
-// over the 16 lanes with xor shuffles; the fp32 quotient is act_quotient
+// over the 16 lanes (one DPP row, row_max16); the fp32 quotient is act_quotient
 // (exact E4M3 codes of the IEEE quotient); the encode is the gfx950
 // v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN), which equals
 // e4m3_rne for every |v| <= 464 -- and |x / s| < 464 always holds because
@@ -37,8 +53,7 @@ __device__ inline uint2 quant_group8(uint4 raw, bool live, bool half, float* sca
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+  amax = row_max16(amax);
   const float s = act_scale(amax);
   const float r = 1.0f / s;  // IEEE division, once per lane
   float q[8];
@@ -61,6 +76,12 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
                         float* scales_out, int64_t n_scales, uint32_t* flags, unsigned long long* rounded,
                         hipStream_t stream);
 
+// Fragment-packed weights: for 16-row tile t and group g a 2 KB block at
+// (t * G + g) * 2048; piece (h, l) at h*1024 + 16 l = bytes [128 g + 32 (l/16)
+// + 16 h, +16) of row 16 t + l%16, zeros past N.  K % 128 == 0.
+inline int64_t packed_weight_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * 16 * K; }
+hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, hipStream_t stream);
+
 // packed: the decode fragment layout (Mpad == 16): group g is 2 KB, the
 // 16-byte piece (h, l) at g*2048 + h*1024 + 16 l holds bytes
 // [32 (l/16) + 16 h, +16) of row l%16.  sa stays [G][Mpad].
@@ -68,11 +89,11 @@ hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mp
                             bool half, bool packed, hipStream_t stream);
 
 // Decode variant shape: NW waves per workgroup (splitting K), R 16-row weight
-// tiles per workgroup.  Chosen by plan_decode_shape.
+// tiles per workgroup, U groups per load step.  Chosen by plan_decode_shape.
 struct DecodeShape {
-  int nw, r;
+  int nw, r, u;
 };
-DecodeShape plan_decode_shape(int N, int G);
+DecodeShape plan_decode_shape(int N, int G, bool packed_weights);
 
 // Quantized activations qa [G][Mpad][128] / sa [G][Mpad] (launch_act_quant)
 // times weight codes w [N, K] with block scales sw [ceil(N/128), G].
@@ -93,6 +114,12 @@ struct GemmArgs {
   // codes, sa [M] per token, sw [N] per output channel, no per-group promotion.
   bool channel = false;
   int64_t ldq = 0;
+  // Weights in the fragment-packed layout of launch_pack_weight (decode and
+  // 256 x 256 kernels only).
+  bool wpack = false;
+  // Decode variant only: qa is the bf16 activation x [M][ldq] (16-byte
+  // aligned rows, ldq % 8 == 0), quantized inside the GEMM (sa unused).
+  bool xq = false;
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);

@@ -79,7 +79,13 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
 // past M re-read row M-1), sa [M], sw [N]; the MFMAs accumulate over all of
 // K and the epilogue applies bf16(fma(p * sa[m], sw[n], bias[n]))
 // (channel_finish.c:9-15).
-template <bool HALF, bool GROUPED, bool CH = false>
+//
+// WPACK: weights in the fragment-packed layout (launch_pack_weight).  Chunk c
+// of row r in group g is piece (c & 1, 16 (c >> 1) + r % 16) of block
+// (r / 16, g); a loader instruction's 8 rows x 8 chunks are then 8 runs of
+// 128 contiguous bytes, as in the row-major layout, and the LDS tile is the
+// same.
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -124,22 +130,26 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ (((r0 + 8 * i) >> 1) & 7)) * 16;
   // Per-lane 32-bit offsets from wave-uniform bases (the loads then use the
   // scalar-base + 32-bit-offset form: fewer VGPRs than 64-bit pointers).
-  const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;
+  const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;  // packed: tile n0/16 starts at (n0/16) * G * 2048 = n0 * K
   const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * (CH ? ldq : 128);
   const int nmax = N - 1 - n0, mmax = M - 1 - m0;
   const uint32_t gstep = CH ? 128u : static_cast<uint32_t>(qstep);  // activation bytes from group to group
   uint32_t aoff[4], boff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    aoff[i] = static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
+    const int ra = min(r0 + 8 * i, nmax), ca = lcs[i] >> 4;
+    aoff[i] = WPACK ? static_cast<uint32_t>(ra >> 4) * static_cast<uint32_t>(G) * 2048u +
+                          static_cast<uint32_t>((ca & 1) * 1024 + ((ca >> 1) * 16 + (ra & 15)) * 16)
+                    : static_cast<uint32_t>(ra * K + lcs[i]);
     boff[i] = CH ? static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i])
                  : static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
   }
+  constexpr uint32_t kAG = WPACK ? 2048u : 128u;  // weight bytes from group to group
   auto issue = [&](int g, int stage) {
     uint8_t* base = smem + stage * kStageBytes + wave * 32 * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_global_load_lds(asrc + static_cast<uint64_t>(aoff[i] + static_cast<uint32_t>(g) * 128u),
+      __builtin_amdgcn_global_load_lds(asrc + static_cast<uint64_t>(aoff[i] + static_cast<uint32_t>(g) * kAG),
                                        base + i * 1024, 16, 0, 0);
       __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g) * gstep),
                                        base + kTile + i * 1024, 16, 0, 0);
@@ -274,31 +284,31 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 // The 128 KB of dynamic LDS is above the default limit: raise it once per device.
 constexpr int kMaxDevices = 64;
 
-std::once_flag g_lds_once[kMaxDevices][8];
-hipError_t g_lds_err[kMaxDevices][8];
+std::once_flag g_lds_once[kMaxDevices][16];
+hipError_t g_lds_err[kMaxDevices][16];
 
-template <bool HALF, bool GROUPED, bool CH = false>
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false>
 hipError_t ensure_lds_limit() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0);
+  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0) + (WPACK ? 8 : 0);
   std::call_once(g_lds_once[dev][slot], [dev] {
     g_lds_err[dev][slot] = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH>),
+        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH, WPACK>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   });
   return g_lds_err[dev][slot];
 }
 
-template <bool HALF, bool GROUPED>
+template <bool HALF, bool GROUPED, bool WPACK = false>
 hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
                      int64_t w_stride, int64_t sw_stride, int kparts, float* yp, hipStream_t stream) {
-  hipError_t e = ensure_lds_limit<HALF, GROUPED>();
+  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK>();
   if (e != hipSuccess) return e;
   const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
-  gemm_prefill256_kernel<HALF, GROUPED><<<tiles * kparts, 512, kLdsBytes, stream>>>(
+  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK><<<tiles * kparts, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
       w_stride, sw_stride, kparts, yp);
   return hipGetLastError();
@@ -324,6 +334,9 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
 // padded with zero rows up to Mpad).
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
   if (a.Mpad % kBM != 0 || !prefill256_fits(a)) return hipErrorInvalidValue;
+  if (a.wpack)
+    return a.half_w ? launch256<true, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream)
+                    : launch256<false, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream);
   return a.half_w ? launch256<true, false>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream)
                   : launch256<false, false>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream);
 }
@@ -333,7 +346,7 @@ hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
 hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt,
                                   int n_groups, int kparts, float* yp, hipStream_t stream) {
   if (a.Mpad % kBM != 0 || n_groups < 1 || kparts < 1 || kparts > 2 || (kparts > 1 && !yp) || (yp && a.N % 4) ||
-      !prefill256_fits(a))
+      !prefill256_fits(a) || a.wpack)
     return hipErrorInvalidValue;
   const int64_t w_stride = static_cast<int64_t>(a.N) * a.K;
   const int64_t sw_stride = static_cast<int64_t>((a.N + 127) / 128) * a.G;

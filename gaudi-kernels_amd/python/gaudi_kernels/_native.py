@@ -43,6 +43,7 @@ GK_FLAG_FORCE_DECODE = 2
 GK_FLAG_FORCE_PREFILL = 4
 GK_FLAG_FORCE_GENERIC = 8
 GK_FLAG_DECODE_LAYOUT = 16
+GK_FLAG_WEIGHT_PACKED = 32
 
 GK_VARIANT_DECODE = 1
 GK_VARIANT_PREFILL = 2
@@ -64,6 +65,8 @@ SIGNATURES = {
     "gk_fp8_codec_ocp_to_half": (_c_int, [_c_vp, _c_vp, _c_i64, _fp, _fp, _c_i64, ctypes.POINTER(_c_i64),
                                           _c_vp, _c_size, _c_vp]),
     "gk_fp8_codec_half_to_ocp": (_c_int, [_c_vp, _c_vp, _c_i64, _fp, _fp, _c_i64, _c_vp, _c_size, _c_vp]),
+    "gk_fp8_packed_weight_bytes": (_c_int, [_c_i64, _c_i64, ctypes.POINTER(_c_size)]),
+    "gk_fp8_pack_weight": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_size, _c_vp]),
     "gk_fp8_act_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _fp, _c_i64, _c_u32, _c_vp]),
     "gk_fp8_block_gemm_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_u32, _c_vp, ctypes.POINTER(_c_int),
                                         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_size)]),

@@ -123,8 +123,57 @@ def decode_layout_to_standard(q):
     return q.reshape(g, 2, 4, 16, 16).permute(0, 3, 2, 1, 4).reshape(g, 16, 128)
 
 
-def _check_gemm_operands(weight, scales, bias, device):
+class PackedWeight:
+    """E4M3 weight codes [n, k] in the fragment-packed device layout of gk_fp8_pack_weight.
+
+    The load-time packing step that fp8_codec.py:19 leaves to the loader.  Pass it wherever a
+    block-FP8 GEMM takes a weight; results are bit-identical to those on the row-major codes.
+    """
+
+    def __init__(self, data, n, k):
+        self.data, self.n, self.k = data, n, k
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+
+def packed_weight_bytes(n, k):
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    nat.check("gk_fp8_packed_weight_bytes", lib.gk_fp8_packed_weight_bytes(n, k, ctypes.byref(nbytes)))
+    return nbytes.value
+
+
+def pack_weight(weight):
+    """Row-major E4M3 codes [N, K] (K % 128 == 0) on the GPU -> PackedWeight (asynchronous)."""
+    device = require_device(weight.device)
     if weight.dtype not in (torch.float8_e4m3fn, torch.uint8) or weight.ndim != 2 or not weight.is_contiguous():
+        raise ValueError("expected a contiguous 2-D E4M3 weight [N, K]")
+    n, k = weight.shape
+    data = torch.empty(packed_weight_bytes(n, k), dtype=torch.uint8, device=device)
+    lib = nat.load()
+    nat.check("gk_fp8_pack_weight",
+              lib.gk_fp8_pack_weight(_ptr(_u8(weight)), n, k, _ptr(data), data.numel(), _stream(device)))
+    return PackedWeight(data, n, k)
+
+
+def _weight_args(weight):
+    """(uint8 tensor passed as w, n, k, extra flags) for a row-major or packed weight."""
+    if isinstance(weight, PackedWeight):
+        return weight.data, weight.n, weight.k, nat.GK_FLAG_WEIGHT_PACKED
+    return _u8(weight), weight.shape[0], weight.shape[1], 0
+
+
+def _check_gemm_operands(weight, scales, bias, device):
+    if isinstance(weight, PackedWeight):
+        if weight.data.dtype != torch.uint8 or weight.data.numel() < packed_weight_bytes(weight.n, weight.k):
+            raise ValueError("PackedWeight data is not a pack_weight output")
+    elif weight.dtype not in (torch.float8_e4m3fn, torch.uint8) or weight.ndim != 2 or not weight.is_contiguous():
         raise ValueError("expected a contiguous 2-D E4M3 weight [N, K]")
     if scales.dtype != torch.float32 or scales.ndim != 2 or not scales.is_contiguous():
         raise ValueError("expected contiguous fp32 block scales [ceil(N/128), ceil(K/128)]")
@@ -137,7 +186,8 @@ def _check_gemm_operands(weight, scales, bias, device):
 def block_fp8_gemm(x, weight, scales, bias=None, *, native_half=False, variant=None, out=None, workspace=None):
     """y = block-FP8 W8A8 linear of bf16 x [M, K] with E4M3 weight [N, K] -> bf16 [M, N] (asynchronous).
 
-    variant: None (dispatch by M), "decode", "prefill" or "generic".
+    weight: row-major codes or a PackedWeight (pack_weight).
+    variant: None (dispatch by M), "decode", "prefill" or "generic" (not for packed weights).
     workspace: optional 256-byte aligned uint8 device tensor of at least plan(...)[2] bytes
     (make_workspace); calls that share one workspace must be ordered on one stream.  Default: the
     cached per-stream workspace().
@@ -147,11 +197,10 @@ def block_fp8_gemm(x, weight, scales, bias=None, *, native_half=False, variant=N
         raise ValueError("expected a 2-D bf16 activation with unit column stride")
     _check_gemm_operands(weight, scales, bias, device)
     m, k = x.shape
-    n = weight.shape[0]
-    if weight.shape[1] != k:
+    w8, n, kw, wflag = _weight_args(weight)
+    if kw != k:
         raise ValueError("activation and weight K differ")
-    flags = _flags(native_half, variant)
-    w8 = _u8(weight)
+    flags = _flags(native_half, variant) | wflag
     _, _, ws_bytes = plan(m, n, k, flags, w8)
     ws = _checked_workspace(workspace, ws_bytes, device)
     if out is None:
@@ -182,9 +231,8 @@ def block_fp8_gemm_q(q, sa, m, weight, scales, bias=None, *, native_half=False, 
     """
     device = require_device(q.device)
     _check_gemm_operands(weight, scales, bias, device)
-    n, k = weight.shape
-    flags = _flags(native_half, variant) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
-    w8 = _u8(weight)
+    w8, n, k, wflag = _weight_args(weight)
+    flags = _flags(native_half, variant) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0) | wflag
     g = (k + 127) // 128
     if q.shape != (g, q.shape[1], 128) or sa.shape != (g, q.shape[1]) or not (q.is_contiguous() and sa.is_contiguous()):
         raise ValueError("expected group-major q [G, m_pad, 128] and sa [G, m_pad] from act_quant")

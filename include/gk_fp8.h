@@ -60,6 +60,7 @@ typedef enum gk_status {
 #define GK_FLAG_FORCE_PREFILL 4u   /* force the LDS-tiled MFMA variant */
 #define GK_FLAG_FORCE_GENERIC 8u   /* force the any-shape variant */
 #define GK_FLAG_DECODE_LAYOUT 16u  /* act_quant / q GEMM only: quantized activations in the decode fragment layout */
+#define GK_FLAG_WEIGHT_PACKED 32u  /* block GEMMs: `w` holds weights packed by gk_fp8_pack_weight (not the generic variant) */
 
 /* Variants reported by gk_fp8_block_gemm_plan. */
 #define GK_VARIANT_DECODE 1
@@ -103,6 +104,25 @@ gk_status gk_fp8_codec_half_to_ocp(const void* src, void* dst, int64_t n, const 
                                    float* scales_out, int64_t n_scales, void* workspace, size_t workspace_bytes,
                                    void* stream);
 
+/* ---- load-time weight packing ------------------------------------------------------ */
+
+/* The layout packing step that fp8_codec.py:19 leaves to the loader ("layout
+ * packing is a separate step"; the Gaudi2 runtime packs to [G, N, 128]).
+ * Here the packed layout is the fragment order of the gfx950 FP8 matrix
+ * instructions: for each 16-row tile t < ceil(n/16) and 128-K group g < k/128
+ * a 2 KB block at (t * G + g) * 2048 whose 16-byte piece (h, l), h < 2,
+ * l < 64, at h*1024 + 16 l holds bytes [128 g + 32 (l/16) + 16 h, +16) of
+ * row 16 t + l%16 (zeros for rows >= n).  Each wave of the GEMM kernels then
+ * reads a tile's group as two contiguous 1 KB loads.  Requires k % 128 == 0.
+ * Block scales are not packed.  Codes are copied unchanged (OCP or half
+ * range alike). */
+gk_status gk_fp8_packed_weight_bytes(int64_t n, int64_t k, size_t* bytes);
+
+/* w E4M3 codes [n, k] (row stride k) -> packed (packed_bytes >= the size
+ * above, 16-byte aligned).  Stream-ordered, no synchronization. */
+gk_status gk_fp8_pack_weight(const void* w, int64_t n, int64_t k, void* packed, size_t packed_bytes,
+                             void* stream);
+
 /* ---- activation quantization ------------------------------------------------ */
 
 /* Per-row 1x128 E4M3 quantization with the oracle's scale rule
@@ -135,7 +155,9 @@ gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags
  * M <= 16 streams weights (decode), larger M runs the LDS-tiled MFMA kernel
  * (prefill).  The activations are quantized into the workspace first.  scale_rows x scale_cols must equal ceil(n/128) x ceil(k/128)
  * (GK_INCOMPATIBLE_INPUT_SIZE otherwise, as generic_fp8_glue_test.cpp:98-100).
- * bias may be NULL.  Inputs are not checked for NaN (see gk_fp8_check_inputs). */
+ * bias may be NULL.  Inputs are not checked for NaN (see gk_fp8_check_inputs).
+ * GK_FLAG_WEIGHT_PACKED: w is gk_fp8_pack_weight's output for (n, k); the
+ * results are bit-identical to those on the row-major weights. */
 gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
                                  const float* scales, int64_t scale_rows, int64_t scale_cols, const float* bias,
                                  void* y, int64_t ldy, uint32_t flags, void* workspace, size_t workspace_bytes,
