@@ -38,8 +38,9 @@ METRIC = "block-FP8 GEMM GB/s & TFLOP/s (% roofline) at M=1..16 and M=4096"
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5033.0   # dense, 256 CU x 8192 FLOP/clk x 2.4 GHz
 MALL_ROTATE_BYTES = 512 << 20
-# The dominant kernel: the decode GEMM instance config 2 runs on packed weights (NW=8, R=2, U=4, QPACK, WPACK).
-DECODE_KERNEL = "gk::gemm_decode_kernel<8,2,4,false,true,false,true>"
+# The roofline kernel: the decode GEMM on pre-quantized activations (decode layout) and packed weights at
+# config 2 (NW=8, R=2, U=4, QPACK, WPACK, no fused quantizer).
+DECODE_KERNEL = "gk::gemm_decode_kernel<8,2,4,false,true,false,true,false>"
 
 
 def gemm_bytes(m, n, k, bias=False):

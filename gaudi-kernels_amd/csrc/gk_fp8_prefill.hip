@@ -80,11 +80,12 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
 // K and the epilogue applies bf16(fma(p * sa[m], sw[n], bias[n]))
 // (channel_finish.c:9-15).
 //
-// WPACK: weights in the fragment-packed layout (launch_pack_weight).  Chunk c
-// of row r in group g is piece (c & 1, 16 (c >> 1) + r % 16) of block
-// (r / 16, g); a loader instruction's 8 rows x 8 chunks are then 8 runs of
-// 128 contiguous bytes, as in the row-major layout, and the LDS tile is the
-// same.
+// WPACK: weights in the fragment-packed layout (launch_pack_weight): chunk c
+// of row r in group g is piece (c & 1, 16 (c >> 1) + r % 16) of the 2 KB
+// block (r / 16, g).  The weight tile is kept in LDS in that packed order, so
+// each loader instruction copies 1 KB of contiguous global memory (wave w:
+// blocks 2w and 2w + 1), and a fragment's two chunks (fc, fc + 1) are the
+// pieces h = 0, 1 of one lane slot, 1024 bytes apart.
 template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
@@ -137,10 +138,11 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   uint32_t aoff[4], boff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int ra = min(r0 + 8 * i, nmax), ca = lcs[i] >> 4;
-    aoff[i] = WPACK ? static_cast<uint32_t>(ra >> 4) * static_cast<uint32_t>(G) * 2048u +
-                          static_cast<uint32_t>((ca & 1) * 1024 + ((ca >> 1) * 16 + (ra & 15)) * 16)
-                    : static_cast<uint32_t>(ra * K + lcs[i]);
+    // packed: block 2 wave + i/2 of the tile (blocks past the last re-read the last one), half i % 2
+    const int blk = min(2 * wave + (i >> 1), ((N + 15) >> 4) - 1 - (n0 >> 4));
+    aoff[i] = WPACK ? static_cast<uint32_t>(blk) * static_cast<uint32_t>(G) * 2048u +
+                          static_cast<uint32_t>((i & 1) * 1024 + lane * 16)
+                    : static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
     boff[i] = CH ? static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i])
                  : static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
   }
@@ -160,8 +162,13 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const int fr = lane & 31, fc = (lane >> 5) * 2, kf = (fr >> 1) & 7;
   const uint32_t xo00 = ((0 + fc) ^ kf) << 4, xo01 = ((1 + fc) ^ kf) << 4;
   const uint32_t xo10 = ((4 + fc) ^ kf) << 4, xo11 = ((5 + fc) ^ kf) << 4;
+  // packed weight tile: row ra = wn*64 + fr, chunk fc + h (+4 for the second K half) ->
+  // (ra/16)*2048 + h*1024 + 16*(16*((fc + 4k)/2) + ra%16)
+  const uint32_t pa = ((wn * 64 + fr) >> 4) * 2048 + 16 * (16 * (lane >> 5) + (fr & 15));
+  const uint32_t ya00 = WPACK ? 0u : xo00, ya01 = WPACK ? 1024u : xo01;
+  const uint32_t ya10 = WPACK ? 512u : xo10, ya11 = WPACK ? 1536u : xo11;
   const uint32_t lbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
-  const uint32_t arow = (wn * 64 + fr) * 128, brow = kTile + (wm * 128 + fr) * 128;
+  const uint32_t arow = WPACK ? pa : (wn * 64 + fr) * 128, brow = kTile + (wm * 128 + fr) * 128;
   const float* sap = sa + (m0 + wm * 128 + fr);  // + 32 j + g * Mpad  (m0 + 256 <= Mpad)
   const float* swp = sw + static_cast<int64_t>(min(n0 + wn * 64, N - 1) >> 7) * G;
 
@@ -189,8 +196,8 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     if (jlive == 0) continue;  // no live rows for this wave (it still takes part in the loads and barriers)
     const uint32_t A = lbase + stage * kStageBytes + arow;
     const uint32_t B = lbase + stage * kStageBytes + brow;
-    v8i a00 = lds_frag(A + xo00, A + xo01), a01 = lds_frag(A + xo10, A + xo11);
-    v8i a10 = lds_frag(A + 4096 + xo00, A + 4096 + xo01), a11 = lds_frag(A + 4096 + xo10, A + 4096 + xo11);
+    v8i a00 = lds_frag(A + ya00, A + ya01), a01 = lds_frag(A + ya10, A + ya11);
+    v8i a10 = lds_frag(A + 4096 + ya00, A + 4096 + ya01), a11 = lds_frag(A + 4096 + ya10, A + 4096 + ya11);
     v8i b0 = lds_frag(B + xo00, B + xo01), b1 = lds_frag(B + xo10, B + xo11);
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a00), "+v"(a01), "+v"(a10), "+v"(a11), "+v"(b0), "+v"(b1));
     if (HALF) {
