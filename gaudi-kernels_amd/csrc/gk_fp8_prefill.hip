@@ -147,14 +147,20 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
                  : static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
   }
   constexpr uint32_t kAG = WPACK ? 2048u : 128u;  // weight bytes from group to group
+  // Activation rows [32 wave, +32) past the tile's live rows are never read
+  // (every wave skips its 32-row blocks past them): their copies are skipped.
+  const bool act_live = wave * 32 < live;  // wave-uniform
   auto issue = [&](int g, int stage) {
     uint8_t* base = smem + stage * kStageBytes + wave * 32 * 128;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_global_load_lds(asrc + static_cast<uint64_t>(aoff[i] + static_cast<uint32_t>(g) * kAG),
                                        base + i * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g) * gstep),
-                                       base + kTile + i * 1024, 16, 0, 0);
+    if (act_live) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g) * gstep),
+                                         base + kTile + i * 1024, 16, 0, 0);
     }
   };
 
