@@ -142,9 +142,15 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
   p->q_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 128);
   p->sa_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 4);
   if (variant == GK_VARIANT_DECODE) p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g), wpack);
-  // Packed weights at M > 16 run the 256 x 256 kernel, which addresses its panels with 32-bit offsets.
-  if (wpack && variant == GK_VARIANT_PREFILL && (p->m_pad * g * 128 > int64_t{0xffffffff} || 256 * k > int64_t{0xffffffff}))
-    return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  // The prefill variant (256 x 256 kernel) addresses its panels with 32-bit
+  // offsets: larger shapes run the generic variant (packed weights: rejected).
+  if (variant == GK_VARIANT_PREFILL && (p->m_pad * g * 128 > int64_t{0xffffffff} || 256 * k > int64_t{0xffffffff})) {
+    if (wpack || force == GK_FLAG_FORCE_PREFILL) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+    p->variant = GK_VARIANT_GENERIC;
+    p->m_pad = m;
+    p->q_bytes = align256(static_cast<size_t>(m) * static_cast<size_t>(g) * 128);
+    p->sa_bytes = align256(static_cast<size_t>(m) * static_cast<size_t>(g) * 4);
+  }
   return GK_SUCCESS;
 }
 

@@ -242,125 +242,6 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// Prefill variant: LDS-tiled, double-buffered.  Workgroup tile 128 weight rows
-// x 128 tokens, K step 128 (one scale group), 4 waves in a 2x2 grid, each
-// wave 64 x 64 = 4 x 4 MFMA tiles.  Tiles are stored in LDS as 128 rows x 128
-// bytes with the 16-byte chunk index XOR-swizzled by (row & 7) so that the 16
-// lanes reading one column chunk of 16 consecutive rows hit distinct banks.
-constexpr int kPB = 128;  // tile edge (rows of W, rows of qa, K bytes)
-
-__device__ inline int swz(int row, int chunk) { return row * kPB + ((chunk ^ (row & 7)) << 4); }
-
-template <bool HALF_W>
-__global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __restrict__ qa,
-                                                           const float* __restrict__ sa,
-                                                           const uint8_t* __restrict__ w,
-                                                           const float* __restrict__ sw,
-                                                           const float* __restrict__ bias,
-                                                           uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                           int K, int G, int Mpad) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][kPB * kPB];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave & 1, wm = wave >> 1;
-  const int n0 = blockIdx.x * kPB, m0 = blockIdx.y * kPB;
-  const int64_t qstep = static_cast<int64_t>(Mpad) * 128;  // one group of qa [G][Mpad][128]
-
-  // Global -> LDS staging: chunk c = tid + 256 i, row = c / 8, 16-byte chunk = c % 8.
-  const int lrow = tid >> 3, lkc = tid & 7;
-  const uint8_t* wsrc[4];
-  const uint8_t* qsrc[4];
-  int soff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = lrow + 32 * i;
-    wsrc[i] = w + static_cast<int64_t>(min(n0 + r, N - 1)) * K + lkc * 16;
-    qsrc[i] = qa + static_cast<int64_t>(m0 + r) * 128 + lkc * 16;
-    soff[i] = swz(r, lkc);
-  }
-  // Fragment reads.
-  const int fr = lane & 15, fk = (lane >> 4) * 2;
-  int aoff[4][2], boff[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ra = wn * 64 + i * 16 + fr, rb = wm * 64 + i * 16 + fr;
-    aoff[i][0] = swz(ra, fk); aoff[i][1] = swz(ra, fk + 1);
-    boff[i][0] = swz(rb, fk); boff[i][1] = swz(rb, fk + 1);
-  }
-  const float* sap[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sap[j] = sa + (m0 + wm * 64 + j * 16 + fr);  // + g * Mpad
-  const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
-
-  v4f acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-
-  uint4 wreg[4], qreg[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    wreg[i] = *reinterpret_cast<const uint4*>(wsrc[i]);
-    qreg[i] = *reinterpret_cast<const uint4*>(qsrc[i]);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<uint4*>(&smem[0][0][soff[i]]) = wreg[i];
-    *reinterpret_cast<uint4*>(&smem[0][1][soff[i]]) = qreg[i];
-  }
-  __syncthreads();
-
-  for (int g = 0; g < G; ++g) {
-    const int buf = g & 1;
-    if (g + 1 < G) {
-      const int64_t koff = static_cast<int64_t>(g + 1) * 128;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        wreg[i] = *reinterpret_cast<const uint4*>(wsrc[i] + koff);
-        qreg[i] = *reinterpret_cast<const uint4*>(qsrc[i] + (g + 1) * qstep);
-      }
-    }
-    const float swg = HALF_W ? 2.0f * swp[g] : swp[g];  // native_half: scales x2
-    float f[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f[j] = sap[j][static_cast<int64_t>(g) * Mpad] * swg;
-    v8i bfr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bfr[j] = pack8(*reinterpret_cast<const uint4*>(&smem[buf][1][boff[j][0]]),
-                     *reinterpret_cast<const uint4*>(&smem[buf][1][boff[j][1]]));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const v8i afr = weight_frag<HALF_W>(*reinterpret_cast<const uint4*>(&smem[buf][0][aoff[i][0]]),
-                                          *reinterpret_cast<const uint4*>(&smem[buf][0][aoff[i][1]]));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4f t = mfma_f8(afr, bfr[j]);
-        acc[i][j][0] = fmaf(t[0], f[j], acc[i][j][0]);
-        acc[i][j][1] = fmaf(t[1], f[j], acc[i][j][1]);
-        acc[i][j][2] = fmaf(t[2], f[j], acc[i][j][2]);
-        acc[i][j][3] = fmaf(t[3], f[j], acc[i][j][3]);
-      }
-    }
-    if (g + 1 < G) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<uint4*>(&smem[buf ^ 1][0][soff[i]]) = wreg[i];
-        *reinterpret_cast<uint4*>(&smem[buf ^ 1][1][soff[i]]) = qreg[i];
-      }
-    }
-    __syncthreads();
-  }
-
-  const int quad = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      store_tile(y, ldy, bias, M, N, m0 + wm * 64 + j * 16 + fr, n0 + wn * 64 + i * 16 + 4 * quad, acc[i][j]);
-}
-
-// ---------------------------------------------------------------------------
 // Generic variant for shapes the tiled kernels do not take (K % 128 != 0 or
 // misaligned weights): one thread per output, byte loads with K bounds.
 __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __restrict__ qa,
@@ -454,18 +335,12 @@ hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
-  // M > 128: 256 x 256 tiles (gk_fp8_prefill.hip); smaller M wastes less on 128 x 128 tiles.
-  // The 256 kernel addresses each operand panel with 32-bit offsets.
-  if ((a.M > 128 || a.wpack) && prefill256_fits(a)) return launch_gemm_prefill256(a, stream);
-  if (a.wpack) return hipErrorInvalidValue;  // packed weights: 256 x 256 kernel only
-  const dim3 grid((a.N + kPB - 1) / kPB, (a.M + kPB - 1) / kPB);
-  if (a.half_w)
-    gemm_prefill_kernel<true><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,
-                                                        a.K, a.G, a.Mpad);
-  else
-    gemm_prefill_kernel<false><<<grid, 256, 0, stream>>>(a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N,
-                                                         a.K, a.G, a.Mpad);
-  return hipGetLastError();
+  // 256 x 256 tiles (gk_fp8_prefill.hip) at every M > 16: they skip the 32-row
+  // blocks past M.  (A 128 x 128 kernel measured 1.2-3x slower at 16 < M <= 128
+  // on MI355X.)  The plan sends shapes whose panels exceed the kernel's 32-bit
+  // offsets to the generic variant.
+  if (!prefill256_fits(a)) return hipErrorInvalidValue;
+  return launch_gemm_prefill256(a, stream);
 }
 
 hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream) {
