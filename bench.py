@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|mlp|moe]
 
-Workload (one "step"): the BASELINE configs[1] decode sweep -- one block-FP8
+Workload (one "step"): BASELINE.json configs[1] decode sweep -- one block-FP8
 GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
 E4M3 weights with fp32 128x128 block scales, bf16 activations quantized per
 1x128 group inside the op, bf16 output.  Inputs are synthetic (seeded
@@ -216,8 +216,8 @@ def main():
         rocprof_summary(args.rocprof_summary)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU runs its own shard, "
-              "see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (under tensor parallelism each GPU "
+              "runs this GEMM on its own shard of the weights); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     from gaudi_kernels import ops

@@ -34,7 +34,7 @@ constexpr const char* kOps[] = {
     "gk_silu_and_mul_bf16_v1",      // silu_and_mul_bf16.c, glue generic_dense_glue.cpp:196-236
     "gk_fp8_silu_mul_quant_bf16_v1",  // SiLU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
-    "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (BASELINE config 5, build-defined)
+    "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (BASELINE.json config 5, build-defined)
     "gk_fp8_pack_weight_v1",        // load-time layout packing (fp8_codec.py:19 "a separate step")
 };
 constexpr uint32_t kNumOps = sizeof(kOps) / sizeof(kOps[0]);
@@ -129,19 +129,20 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
   } else if (force == GK_FLAG_FORCE_PREFILL) {
     variant = GK_VARIANT_PREFILL;
   } else if (force == GK_FLAG_FORCE_DECODE) {
-    if (m > gk::kDecodeMaxRows) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+    if (m > gk::kDecodeMaxTokens) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
     variant = GK_VARIANT_DECODE;
   } else {
-    variant = m <= gk::kDecodeMaxRows ? GK_VARIANT_DECODE : GK_VARIANT_PREFILL;
+    variant = m <= gk::kDecodeMaxTokens ? GK_VARIANT_DECODE : GK_VARIANT_PREFILL;
   }
   *p = Plan();
   p->variant = variant;
-  p->m_pad = variant == GK_VARIANT_DECODE    ? gk::kDecodeMaxRows
+  p->m_pad = variant == GK_VARIANT_DECODE    ? 16 * gk::decode_tiles(m)
              : variant == GK_VARIANT_PREFILL ? round_up(m, gk::kPrefillRowTile)
                                              : m;
   p->q_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 128);
   p->sa_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 4);
-  if (variant == GK_VARIANT_DECODE) p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g), wpack);
+  if (variant == GK_VARIANT_DECODE)
+    p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g), wpack, gk::decode_tiles(m));
   // The prefill variant (256 x 256 kernel) addresses its panels with 32-bit
   // offsets: larger shapes run the generic variant (packed weights: rejected).
   if (variant == GK_VARIANT_PREFILL && (p->m_pad * g * 128 > int64_t{0xffffffff} || 256 * k > int64_t{0xffffffff})) {
@@ -291,7 +292,7 @@ gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx
   if (m_pad < m || m_pad > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
   if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_DECODE_LAYOUT}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
   const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
-  if (packed && m_pad != gk::kDecodeMaxRows) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (packed && m_pad != 16 && m_pad != 32 && m_pad != 64) return GK_INCOMPATIBLE_OUTPUT_SIZE;
   if ((reinterpret_cast<uintptr_t>(x) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
       (reinterpret_cast<uintptr_t>(sa) & 3))
     return GK_INCOMPATIBLE_DATA_TYPE;
@@ -353,8 +354,8 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
   // Decode variant with 16-byte aligned activation rows and little redundant
   // quantization work: the GEMM quantizes x itself (one launch, the same
   // codes and scales as the quantizer below).
-  if (p.variant == GK_VARIANT_DECODE && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 8 == 0 &&
-      fused_quant_pays(m, n, k, p.dec))
+  if (p.variant == GK_VARIANT_DECODE && p.dec.mt == 1 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+      ldx % 8 == 0 && fused_quant_pays(m, n, k, p.dec))
     return run_gemm(p, static_cast<const uint8_t*>(x), nullptr, m, k, w, n, scales, bias, y, ldy, flags, false, s,
                     ldx);
   uint8_t* q = static_cast<uint8_t*>(workspace);
@@ -494,7 +495,7 @@ gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t 
   if (m_pad < rows || m_pad > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
   if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_DECODE_LAYOUT}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
   const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
-  if (packed && m_pad != gk::kDecodeMaxRows) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (packed && m_pad != 16 && m_pad != 32 && m_pad != 64) return GK_INCOMPATIBLE_OUTPUT_SIZE;
   if ((reinterpret_cast<uintptr_t>(gate_up) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
       (reinterpret_cast<uintptr_t>(sa) & 3))
     return GK_INCOMPATIBLE_DATA_TYPE;

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(const uint16_t* __res
 
 // Fused: 16 lanes per (row, 128-column group), 8 columns per lane.  Output as
 // act_quant_kernel: group-major q [G][Mpad][128] / sa [G][Mpad] (rows >= rows
-// zero) or, PACKED, the decode fragment layout (Mpad == 16).
+// zero) or, PACKED, the decode fragment layout (Mpad = 16, 32 or 64).
 template <bool HALF, bool PACKED>
 __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ in, int64_t ldi, int rows,
                                                              int width, int G, int Mpad, uint8_t* __restrict__ q,
@@ -83,9 +83,7 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __r
   const uint2 codes = quant_group8(raw, live, HALF, &s);  // all 16 lanes of a group take part
   if (active) {
     const int64_t slot = static_cast<int64_t>(g) * Mpad + row;
-    const int64_t at = PACKED ? static_cast<int64_t>(g) * 2048 + ((sub >> 1) & 1) * 1024 +
-                                    (16 * (sub >> 2) + row) * 16 + (sub & 1) * 8
-                              : slot * 128 + sub * 8;
+    const int64_t at = PACKED ? decode_layout_offset(g, row, 8 * sub, Mpad) : slot * 128 + sub * 8;
     *reinterpret_cast<uint2*>(q + at) = live ? codes : make_uint2(0u, 0u);
     if (sub == 0) sa[slot] = live ? s : 0.0f;
   }
@@ -105,7 +103,7 @@ hipError_t launch_silu_and_mul(const uint16_t* in, int64_t ldi, int rows, int wi
 
 hipError_t launch_silu_mul_act_quant(const uint16_t* in, int64_t ldi, int rows, int width, int Mpad, uint8_t* q,
                                      float* sa, bool half, bool packed, hipStream_t stream) {
-  if (packed && Mpad != kDecodeMaxRows) return hipErrorInvalidValue;
+  if (packed && Mpad != 16 && Mpad != 32 && Mpad != 64) return hipErrorInvalidValue;
   const int G = (width + 127) / 128;
   const int64_t groups = static_cast<int64_t>(Mpad) * G;
   const unsigned blocks = static_cast<unsigned>((groups + 15) / 16);

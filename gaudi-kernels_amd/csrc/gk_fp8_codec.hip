@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void codec_scales_kernel(const float* __restri
 // reference quant op's {128, R, G} layout): q [G][Mpad][128] codes (rows >= M
 // and columns >= K are written as zero), sa [G][Mpad] fp32 (zero for rows >=
 // M).  One group = 16 lanes x 8 elements (quant_group8).  PACKED writes q in
-// the decode fragment layout instead (Mpad == 16; gk_fp8_internal.h).
+// the decode fragment layout instead (Mpad = 16, 32 or 64; gk_fp8_internal.h).
 template <bool HALF, bool PACKED>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                         int K, int G, int Mpad, uint8_t* __restrict__ q,
@@ -170,9 +170,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   if (active) {
     const int64_t slot = static_cast<int64_t>(g) * Mpad + row;
     // bytes [8 sub, 8 sub + 8): 16-byte chunk c = sub / 2 goes to piece (c % 2, 16 (c / 2) + row)
-    const int64_t at = PACKED ? static_cast<int64_t>(g) * 2048 + ((sub >> 1) & 1) * 1024 +
-                                    (16 * (sub >> 2) + row) * 16 + (sub & 1) * 8
-                              : slot * 128 + sub * 8;
+    const int64_t at = PACKED ? decode_layout_offset(g, row, 8 * sub, Mpad) : slot * 128 + sub * 8;
     *reinterpret_cast<uint2*>(q + at) = live ? codes : make_uint2(0u, 0u);
     if (sub == 0) sa[slot] = live ? s : 0.0f;
   }
@@ -245,7 +243,7 @@ hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, h
 
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
                             bool half, bool packed, hipStream_t stream) {
-  if (packed && Mpad != kDecodeMaxRows) return hipErrorInvalidValue;
+  if (packed && Mpad != 16 && Mpad != 32 && Mpad != 64) return hipErrorInvalidValue;
   const int G = (K + 127) / 128;
   const int64_t groups = static_cast<int64_t>(Mpad) * G;
   const int blocks = static_cast<int>((groups + 15) / 16);  // 16 groups per 256-thread block

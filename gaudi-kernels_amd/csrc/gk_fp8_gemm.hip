@@ -76,7 +76,8 @@ namespace gk {
 // scale per token sa[m] and per output channel sw[n]; the MFMAs accumulate
 // over all of K (no per-group promotion) and the epilogue applies
 // bf16(fma(p * sa[m], sw[n], bias[n])) (channel_finish.c:9-15).
-template <int NW, int R, int U, bool HALF, bool QPACK, bool CH = false, bool WPACK = false, bool XQ = false>
+template <int NW, int R, int U, bool HALF, bool QPACK, bool CH = false, bool WPACK = false, bool XQ = false,
+          int MT = 1>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -85,9 +86,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
                                                               uint16_t* __restrict__ y, int64_t ldy, int M,
                                                               int N, int K, int G, int64_t ldq = 0) {
   static_assert(16 * R <= 128 && NW >= R, "a workgroup's rows lie in one 128-row scale block");
+  static_assert(MT == 1 || (!XQ && !CH), "several token tiles take pre-quantized block-scaled activations");
   __shared__ __attribute__((aligned(16))) uint8_t tile[WPACK ? 1 : NW][2048];
   __shared__ __attribute__((aligned(16))) uint8_t xqbuf[XQ ? NW : 1][XQ ? U : 1][2048 + 64];  // codes + 16 scales
-  __shared__ v4f red[NW][R][64];
+  __shared__ v4f red[NW][R][MT][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int col = lane & 15, quad = lane >> 4;
@@ -112,10 +114,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   const uint32_t woff1 = (lrow + 8) * 128 + ((lch ^ (((lrow + 8) >> 1) & 7)) << 4);
   const uint32_t roff0 = col * 128 + (((2 * quad) ^ ((col >> 1) & 7)) << 4);
   const uint32_t roff1 = col * 128 + (((2 * quad + 1) ^ ((col >> 1) & 7)) << 4);
-  const int tok = min(col, M - 1);
-  const uint8_t* qp = CH      ? qa + tok * ldq + quad * 32
-                      : QPACK ? qa + (16 * quad + tok) * 16
-                              : qa + tok * 128 + quad * 32;
+  // Token tile t holds tokens 16 t .. 16 t + 15; tokens >= M read token M-1.
+  // Decode fragment layout: (group g, token tile tt) is the 2 KB block
+  // g * MT + tt; standard layout: row tok of group g at (g * 16 MT + tok) * 128.
+  const uint8_t* qpt[MT];
+  const float* sapt[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int tk = min(16 * t + col, M - 1);
+    qpt[t] = CH      ? qa + tk * ldq + quad * 32
+             : QPACK ? qa + (tk >> 4) * 2048 + (16 * quad + (tk & 15)) * 16
+                     : qa + tk * 128 + quad * 32;
+    sapt[t] = sa + tk;
+  }
   // XQ loader: load j reads token 4j + lane/16 (tokens >= M re-read token
   // M-1), elements [8 (lane%16), +8) of the group; its 8 codes are bytes
   // e0 = 8 (lane%16) .. e0+7 of that token, which the fragment layout keeps
@@ -132,18 +143,19 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   // fragment columns hold whatever the buffer held and are never stored.
   const int xjn = (min(M, 16) + 3) >> 2;
   constexpr int kQHi = QPACK ? 1024 : 16;
-  constexpr int kQG = CH ? 128 : 2048;              // bytes from one group to the next
-  const float* sap = XQ ? sa : sa + tok;            // + g * 16 (unused with XQ)
+  constexpr int kQG = CH ? 128 : 2048 * MT;         // activation bytes from one group to the next
   const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
   uint8_t* buf = tile[WPACK ? 0 : wave];
 
-  v4f acc[R];
+  v4f acc[R][MT];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[r][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   for (int g0 = gbeg; g0 < gend; g0 += U) {
-    uint4 wa[U][R][2], qb[U][2], xb[XQ ? U : 1][4];
-    float sv[U], wv[U];
+    uint4 wa[U][R][2], qb[U][MT][2], xb[XQ ? U : 1][4];
+    float sv[U][MT], wv[U];
     if (XQ) {  // activations first: they are needed before the weights
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -163,17 +175,23 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
         wa[u][r][1] = load_stream16(p + d8[r]);
       }
       if (!XQ) {
-        const uint8_t* q = qp + static_cast<int64_t>(g) * kQG;
-        qb[u][0] = *reinterpret_cast<const uint4*>(q);
-        qb[u][1] = *reinterpret_cast<const uint4*>(q + kQHi);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const uint8_t* q = qpt[t] + static_cast<int64_t>(g) * kQG;
+          qb[u][t][0] = *reinterpret_cast<const uint4*>(q);
+          qb[u][t][1] = *reinterpret_cast<const uint4*>(q + kQHi);
+        }
       }
       if (!CH) {
-        if (!XQ) sv[u] = sap[g * 16];
+        if (!XQ) {
+#pragma unroll
+          for (int t = 0; t < MT; ++t) sv[u][t] = sapt[t][g * 16 * MT];
+        }
         wv[u] = swp[g];
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the step is in flight before the first use
-    v8i bq[XQ ? U : 1];
+    v8i bq[XQ ? U : 1];  // XQ implies MT == 1
     if (XQ) {
       uint8_t* xq = xqbuf[wave][0];
 #pragma unroll
@@ -191,14 +209,13 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
       for (int u = 0; u < U; ++u) {  // same wave: its LDS accesses complete in order
         const uint8_t* b = xq + u * (2048 + 64);
         bq[u] = pack8(*reinterpret_cast<const uint4*>(b + 16 * lane), *reinterpret_cast<const uint4*>(b + 1024 + 16 * lane));
-        sv[u] = *reinterpret_cast<const float*>(b + 2048 + 4 * col);
+        sv[u][0] = *reinterpret_cast<const float*>(b + 2048 + 4 * col);
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const v8i b = XQ ? bq[u] : pack8(qb[u][0], qb[u][1]);
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-      const float f = CH ? 0.0f : (g0 + u < gend) ? sv[u] * (HALF ? 2.0f * wv[u] : wv[u]) : 0.0f;
+      const float ws = HALF ? 2.0f * wv[u] : wv[u];
       const bool live = g0 + u < gend;  // the clamped repeat of the last group adds nothing
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -209,36 +226,47 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
           lo = *reinterpret_cast<const uint4*>(buf + roff0);
           hi = *reinterpret_cast<const uint4*>(buf + roff1);
         }
-        if (CH) {
-          if (live) acc[r] = mfma_f8_acc(weight_frag<HALF>(lo, hi), b, acc[r]);
-        } else {
-          const v4f t = mfma_f8(weight_frag<HALF>(lo, hi), b);
-          acc[r][0] = fmaf(t[0], f, acc[r][0]);
-          acc[r][1] = fmaf(t[1], f, acc[r][1]);
-          acc[r][2] = fmaf(t[2], f, acc[r][2]);
-          acc[r][3] = fmaf(t[3], f, acc[r][3]);
+        const v8i a = weight_frag<HALF>(lo, hi);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const v8i b = XQ ? bq[u] : pack8(qb[u][t][0], qb[u][t][1]);
+          if (CH) {
+            if (live) acc[r][t] = mfma_f8_acc(a, b, acc[r][t]);
+          } else {
+            const float f = live ? sv[u][t] * ws : 0.0f;
+            const v4f p = mfma_f8(a, b);
+            acc[r][t][0] = fmaf(p[0], f, acc[r][t][0]);
+            acc[r][t][1] = fmaf(p[1], f, acc[r][t][1]);
+            acc[r][t][2] = fmaf(p[2], f, acc[r][t][2]);
+            acc[r][t][3] = fmaf(p[3], f, acc[r][t][3]);
+          }
         }
       }
     }
   }
 #pragma unroll
-  for (int r = 0; r < R; ++r) red[wave][r][lane] = acc[r];
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[wave][r][t][lane] = acc[r][t];
   __syncthreads();
-  if (wave >= R) return;
-  v4f sum = red[0][wave][lane];
+  // wave w sums (tile, token tile) pairs w, w + NW, ... of the NW partials in wave order
+  for (int pr = wave; pr < R * MT; pr += NW) {
+    const int r = pr / MT, t = pr % MT;
+    v4f sum = red[0][r][t][lane];
 #pragma unroll
-  for (int v = 1; v < NW; ++v) sum += red[v][wave][lane];
-  if (CH) {
-    const int n = n0 + 16 * wave + 4 * quad;
-    if (col >= M) return;
-    const float sam = sa[col];
-    uint16_t* row = y + static_cast<int64_t>(col) * ldy + n;
+    for (int v = 1; v < NW; ++v) sum += red[v][r][t][lane];
+    const int m = 16 * t + col, n = n0 + 16 * r + 4 * quad;
+    if (CH) {
+      if (m >= M) continue;
+      const float sam = sa[m];
+      uint16_t* row = y + static_cast<int64_t>(m) * ldy + n;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (n + r < N) row[r] = channel_out(sum[r], sam, sw[n + r], bias ? bias[n + r] : 0.0f);
-    return;
+      for (int i = 0; i < 4; ++i)
+        if (n + i < N) row[i] = channel_out(sum[i], sam, sw[n + i], bias ? bias[n + i] : 0.0f);
+    } else {
+      store_tile(y, ldy, bias, M, N, m, n, sum);
+    }
   }
-  store_tile(y, ldy, bias, M, N, col, n0 + 16 * wave + 4 * quad, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -272,17 +300,17 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const uint8_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-template <int NW, int R, int U>
+template <int NW, int R, int U, int MT>
 static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
 #define GK_DECODE_LAUNCH(H, P, WP, X)                                                                          \
-  gemm_decode_kernel<NW, R, U, H, P, false, WP, X><<<grid, NW * 64, 0, stream>>>(                               \
+  gemm_decode_kernel<NW, R, U, H, P, false, WP, X, MT><<<grid, NW * 64, 0, stream>>>(                               \
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq)
 #define GK_DECODE_LAUNCH_P(H, P, X) \
   if (a.wpack) GK_DECODE_LAUNCH(H, P, true, X); else GK_DECODE_LAUNCH(H, P, false, X)
-#define GK_DECODE_LAUNCH_A(H)                         \
-  if (a.xq) { GK_DECODE_LAUNCH_P(H, false, true); }      \
-  else if (a.qpack) { GK_DECODE_LAUNCH_P(H, true, false); } \
+#define GK_DECODE_LAUNCH_A(H)                                       \
+  if (MT == 1 && a.xq) { GK_DECODE_LAUNCH_P(H, false, MT == 1); }      \
+  else if (a.qpack) { GK_DECODE_LAUNCH_P(H, true, false); }               \
   else { GK_DECODE_LAUNCH_P(H, false, false); }
   if (a.half_w) {
     GK_DECODE_LAUNCH_A(true)
@@ -295,39 +323,48 @@ static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-DecodeShape plan_decode_shape(int N, int G, bool packed_weights) {
+DecodeShape plan_decode_shape(int N, int G, bool packed_weights, int mt) {
   // R: 16-row tiles per workgroup.  Every workgroup reads the activations of
   // its K range once, so larger R cuts activation traffic, but the workgroup
   // count (tiles / R) must stay near or above the 256 CUs.  NW: waves
   // splitting K (the partials are summed in wave order, so NW fixes the
   // result bits; both weight layouts use the same NW for every N and give
-  // identical results).  U: groups per load step.  Measured on MI355X at
-  // M = 16 for N x K = 28672 x 4096, 6144 x 4096, 4096 x 14336; the packed
+  // identical results).  U: groups per load step, divided by the token tiles
+  // mt (each group's activation fragments grow with mt).  Measured on MI355X
+  // at M = 16 for N x K = 28672 x 4096, 6144 x 4096, 4096 x 14336; the packed
   // layout (no LDS transpose) gains from the deeper step at N = 6144.
   (void)G;
   const int tiles = (N + 15) / 16;
-  if (tiles >= 1536) return DecodeShape{2, 2, 4};
-  if (tiles >= 384) return packed_weights ? DecodeShape{8, 2, 4} : DecodeShape{8, 2, 2};
-  if (tiles >= 256) return DecodeShape{8, 1, 2};
-  return DecodeShape{16, 1, 2};
+  DecodeShape d;
+  if (tiles >= 1536) d = DecodeShape{2, 2, 4, 1};
+  else if (tiles >= 384) d = packed_weights ? DecodeShape{8, 2, 4, 1} : DecodeShape{8, 2, 2, 1};
+  else if (tiles >= 256) d = DecodeShape{8, 1, 2, 1};
+  else d = DecodeShape{16, 1, 2, 1};
+  d.mt = mt;
+  d.u = d.u / mt > 0 ? d.u / mt : 1;
+  return d;
 }
 
-template <int NW, int R, int U>
+template <int NW, int R, int U, int MT>
 static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
+  static_assert(MT == 1, "the per-channel decode takes one token tile");
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
   gemm_decode_kernel<NW, R, U, false, false, true><<<grid, NW * 64, 0, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq);
   return hipGetLastError();
 }
 
-// Instantiated decode shapes (NW, R, U); plan_decode_shape returns only these.
-#define GK_DECODE_SHAPES(X) X(2, 2, 4) X(8, 2, 2) X(8, 2, 4) X(8, 1, 2) X(16, 1, 2)
+// Instantiated decode shapes (NW, R, U, MT); plan_decode_shape returns only these.
+#define GK_DECODE_SHAPES1(X) X(2, 2, 4, 1) X(8, 2, 2, 1) X(8, 2, 4, 1) X(8, 1, 2, 1) X(16, 1, 2, 1)
+#define GK_DECODE_SHAPES(X) GK_DECODE_SHAPES1(X)                                               \
+  X(2, 2, 2, 2) X(8, 2, 1, 2) X(8, 2, 2, 2) X(8, 1, 1, 2) X(16, 1, 1, 2)                       \
+  X(2, 2, 1, 4) X(8, 2, 1, 4) X(8, 1, 1, 4) X(16, 1, 1, 4)
+constexpr int decode_key(int nw, int r, int u, int mt) { return ((nw * 10 + r) * 10 + u) * 10 + mt; }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
-  const int key = a.dec.nw * 100 + a.dec.r * 10 + a.dec.u;
-  switch (key) {
-#define GK_CASE(NW, R, U) \
-  case NW * 100 + R * 10 + U: return decode_launch<NW, R, U>(a, stream);
+  switch (decode_key(a.dec.nw, a.dec.r, a.dec.u, a.dec.mt)) {
+#define GK_CASE(NW, R, U, MT) \
+  case decode_key(NW, R, U, MT): return decode_launch<NW, R, U, MT>(a, stream);
     GK_DECODE_SHAPES(GK_CASE)
 #undef GK_CASE
     default: return hipErrorInvalidValue;
@@ -345,11 +382,11 @@ hipError_t launch_gemm_prefill(const GemmArgs& a, hipStream_t stream) {
 
 hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream) {
   if (a.M > kDecodeMaxRows) return launch_gemm_channel256(a, stream);
-  const DecodeShape d = plan_decode_shape(a.N, a.G, false);
-  switch (d.nw * 100 + d.r * 10 + d.u) {
-#define GK_CASE(NW, R, U) \
-  case NW * 100 + R * 10 + U: return decode_channel_launch<NW, R, U>(a, stream);
-    GK_DECODE_SHAPES(GK_CASE)
+  const DecodeShape d = plan_decode_shape(a.N, a.G, false, 1);
+  switch (decode_key(d.nw, d.r, d.u, d.mt)) {
+#define GK_CASE(NW, R, U, MT) \
+  case decode_key(NW, R, U, MT): return decode_channel_launch<NW, R, U, MT>(a, stream);
+    GK_DECODE_SHAPES1(GK_CASE)
 #undef GK_CASE
     default: return hipErrorInvalidValue;
   }

@@ -14,7 +14,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 // Row padding of the quantized-activation workspace.
-constexpr int kDecodeMaxRows = 16;   // decode variant: M <= 16, padded to one MFMA column tile
+constexpr int kDecodeMaxRows = 16;   // one MFMA column tile of tokens (the fused quantizer, per-channel decode)
+constexpr int kDecodeMaxTokens = 64;  // decode variant: M <= 64 in 1, 2 or 4 column tiles (Mpad = 16, 32, 64)
+// Token tiles of the decode variant for M tokens (Mpad = 16 * decode_tiles(M)).
+inline int decode_tiles(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+// Offset of codes byte `e` (0..127) of token `row` in group g of the decode fragment layout with Mpad rows:
+// block (g, row / 16) of 2 KB, piece (h, l) = ((e / 16) & 1, 16 (e / 32) + row % 16), byte e % 16.
+__host__ __device__ inline int64_t decode_layout_offset(int g, int64_t row, int e, int Mpad) {
+  return (static_cast<int64_t>(g) * (Mpad >> 4) + (row >> 4)) * 2048 + ((e >> 4) & 1) * 1024 +
+         (16 * (e >> 5) + (row & 15)) * 16 + (e & 15);
+}
 constexpr int kPrefillRowTile = 256; // prefill variant: M padded to the token tile
 
 // Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in VALU
@@ -82,18 +91,19 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
 inline int64_t packed_weight_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * 16 * K; }
 hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, hipStream_t stream);
 
-// packed: the decode fragment layout (Mpad == 16): group g is 2 KB, the
-// 16-byte piece (h, l) at g*2048 + h*1024 + 16 l holds bytes
-// [32 (l/16) + 16 h, +16) of row l%16.  sa stays [G][Mpad].
+// packed: the decode fragment layout (Mpad = 16, 32 or 64): the 2 KB block
+// (group g, token tile t) at (g * Mpad/16 + t) * 2048 holds, in its 16-byte
+// piece (h, l) at h*1024 + 16 l, bytes [32 (l/16) + 16 h, +16) of row
+// 16 t + l%16 (decode_layout_offset).  sa stays [G][Mpad].
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
                             bool half, bool packed, hipStream_t stream);
 
 // Decode variant shape: NW waves per workgroup (splitting K), R 16-row weight
 // tiles per workgroup, U groups per load step.  Chosen by plan_decode_shape.
 struct DecodeShape {
-  int nw, r, u;
+  int nw, r, u, mt;  // mt: 16-token column tiles
 };
-DecodeShape plan_decode_shape(int N, int G, bool packed_weights);
+DecodeShape plan_decode_shape(int N, int G, bool packed_weights, int mt);
 
 // Quantized activations qa [G][Mpad][128] / sa [G][Mpad] (launch_act_quant)
 // times weight codes w [N, K] with block scales sw [ceil(N/128), G].

@@ -2,7 +2,7 @@
 // quantization, fused SiLU-and-mul + quantization, weighted combine.  The
 // expert GEMMs are the grouped 256 x 256 kernel (gk_fp8_prefill.hip).
 //
-// The reference has no MoE code for this path; the layer follows BASELINE's
+// The reference has no MoE code for this path; the layer follows BASELINE.json's
 // config 5 and is build-defined (the CPU restatement is oracle/moe.py):
 //   * route: top-k (k <= 2) experts by router logit, ties to the lower index;
 //     combine weights = softmax over the k selected logits (fp32);

@@ -97,15 +97,16 @@ def act_quant(x, *, native_half=False, m_pad=None, decode_layout=False):
     """1x128 activation quantization on the GPU -> group-major (codes uint8 [G, m_pad, 128], sa fp32 [G, m_pad]).
 
     The layout of the reference's quant op output ({128, R, G} FCD-first, generic_fp8_glue.hpp:84-109).
-    decode_layout=True (m_pad 16) stores each group's 2 KB of codes in the decode fragment order
-    (include/gk_fp8.h, GK_FLAG_DECODE_LAYOUT) for block_fp8_gemm_q(..., decode_layout=True).
+    decode_layout=True (m_pad 16, 32 or 64 -- by default the decode plan's, 16 * ceil-to-{1,2,4}(M/16)) stores each
+    group's codes in the decode fragment order (include/gk_fp8.h, GK_FLAG_DECODE_LAYOUT) for
+    block_fp8_gemm_q(..., decode_layout=True).
     """
     device = require_device(x.device)
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
         raise ValueError("expected a 2-D bf16 activation with unit column stride")
     m, k = x.shape
     g = (k + 127) // 128
-    m_pad = (16 if decode_layout else m) if m_pad is None else m_pad
+    m_pad = (16 * decode_tiles(m) if decode_layout else m) if m_pad is None else m_pad
     q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
     sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
     flags = (nat.GK_FLAG_NATIVE_HALF if native_half else 0) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
@@ -116,11 +117,17 @@ def act_quant(x, *, native_half=False, m_pad=None, decode_layout=False):
     return q, sa
 
 
+def decode_tiles(m):
+    """16-token column tiles of the decode variant for M <= 64 tokens (its m_pad is 16 times this)."""
+    return 1 if m <= 16 else 2 if m <= 32 else 4
+
+
 def decode_layout_to_standard(q):
-    """View helper: codes in the decode fragment layout [G, 16, 128] -> the standard [G, 16, 128] order."""
-    g = q.shape[0]
-    # piece (h, l) = bytes [32 (l // 16) + 16 h, +16) of row l % 16  ->  [G, h, quad, row, 16]
-    return q.reshape(g, 2, 4, 16, 16).permute(0, 3, 2, 1, 4).reshape(g, 16, 128)
+    """View helper: codes in the decode fragment layout [G, m_pad, 128] -> the standard [G, m_pad, 128] order."""
+    g, m_pad = q.shape[0], q.shape[1]
+    # block (group, token tile t), piece (h, l) = bytes [32 (l // 16) + 16 h, +16) of row 16 t + l % 16
+    # -> [G, t, h, quad, row, 16]
+    return q.reshape(g, m_pad // 16, 2, 4, 16, 16).permute(0, 1, 4, 3, 2, 5).reshape(g, m_pad, 128)
 
 
 class PackedWeight:
@@ -322,7 +329,7 @@ def silu_mul_quant(gate_up, *, native_half=False, m_pad=None, decode_layout=Fals
     device = require_device(gate_up.device)
     rows, width = _check_gate_up(gate_up, device)
     g = (width + 127) // 128
-    m_pad = (16 if decode_layout else rows) if m_pad is None else m_pad
+    m_pad = (16 * decode_tiles(rows) if decode_layout else rows) if m_pad is None else m_pad
     q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
     sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
     flags = (nat.GK_FLAG_NATIVE_HALF if native_half else 0) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)

@@ -56,7 +56,7 @@ typedef enum gk_status {
 
 /* GEMM flags. */
 #define GK_FLAG_NATIVE_HALF 1u     /* block_fp8_oracle.py:31-35: half-range activations and weights, scales x2 */
-#define GK_FLAG_FORCE_DECODE 2u    /* force the M <= 16 weight-streaming variant (requires M <= 16) */
+#define GK_FLAG_FORCE_DECODE 2u    /* force the weight-streaming variant (requires M <= 64) */
 #define GK_FLAG_FORCE_PREFILL 4u   /* force the LDS-tiled MFMA variant */
 #define GK_FLAG_FORCE_GENERIC 8u   /* force the any-shape variant */
 #define GK_FLAG_DECODE_LAYOUT 16u  /* act_quant / q GEMM only: quantized activations in the decode fragment layout */
@@ -96,7 +96,7 @@ gk_status gk_fp8_codec_ocp_to_half(const void* src, void* dst, int64_t n, const 
                                    float* scales_out, int64_t n_scales, int64_t* rounded, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
-/* Inverse codec (no reference function; SURVEY a2'): half-range codes ->
+/* Inverse codec (no reference function): half-range codes ->
  * OCP E4M3FN (value x2, exact), scales / 2.  Magnitudes >= 0x77 have no OCP
  * image -> GK_NONFINITE_CODE; a scale whose half is an inexact fp32
  * subnormal -> GK_INEXACT_SCALE.  Synchronizes `stream`. */
@@ -131,11 +131,12 @@ gk_status gk_fp8_pack_weight(const void* w, int64_t n, int64_t k, void* packed, 
  * generic_fp8_glue.hpp:84-109) in that op's group-major layout ({128, R, G}
  * FCD-first): q codes [G][m_pad][128] (G = ceil(k/128)), sa fp32 [G][m_pad];
  * rows >= m and columns >= k are written as zero.  m_pad >= m.
- * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_DECODE_LAYOUT (m_pad must be 16) writes
- * q in the decode fragment layout the M <= 16 GEMM reads with coalesced
- * loads: group g is 2 KB and the 16-byte piece (h, l), h < 2, l < 64, at
- * g*2048 + h*1024 + 16 l holds bytes [32 (l/16) + 16 h, +16) of row l%16.
- * sa keeps its [G][16] layout. */
+ * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_DECODE_LAYOUT (m_pad must be 16, 32 or
+ * 64: 16 tokens per tile, T = m_pad/16 tiles) writes q in the decode fragment
+ * layout the M <= 64 GEMM reads with coalesced loads: the 2 KB block of group
+ * g and token tile t sits at (g*T + t)*2048, and its 16-byte piece (h, l),
+ * h < 2, l < 64, at + h*1024 + 16 l holds bytes [32 (l/16) + 16 h, +16) of
+ * row 16 t + l%16.  sa keeps its [G][m_pad] layout. */
 gk_status gk_fp8_act_quant_bf16(const void* x, int64_t m, int64_t k, int64_t ldx, void* q, float* sa,
                                 int64_t m_pad, uint32_t flags, void* stream);
 
@@ -152,8 +153,8 @@ gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags
  * gk_fp8_block_reduce_bf16_v1 (reduce_bias.c:204-258) and the prefill chain
  * act_row_scale -> quant_act_fp16_1k -> dequant_weight_fp16_1k -> MME ->
  * epilogue(_bias) (fp8_hybrid_tpcsim_test.cpp:180-324).  Dispatch by M:
- * M <= 16 streams weights (decode), larger M runs the LDS-tiled MFMA kernel
- * (prefill).  The activations are quantized into the workspace first.  scale_rows x scale_cols must equal ceil(n/128) x ceil(k/128)
+ * M <= 64 streams weights (decode: one to four 16-token tiles share each
+ * weight fragment), larger M runs the LDS-tiled MFMA kernel (prefill).  The activations are quantized into the workspace first.  scale_rows x scale_cols must equal ceil(n/128) x ceil(k/128)
  * (GK_INCOMPATIBLE_INPUT_SIZE otherwise, as generic_fp8_glue_test.cpp:98-100).
  * bias may be NULL.  Inputs are not checked for NaN (see gk_fp8_check_inputs).
  * GK_FLAG_WEIGHT_PACKED: w is gk_fp8_pack_weight's output for (n, k); the
@@ -226,15 +227,14 @@ gk_status gk_silu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width,
                                int64_t ld_out, void* stream);
 
 /* The same products quantized per 1x128 group for the next block-FP8 GEMM
- * (no reference op: the fusion SURVEY ranks first among the path's
- * neighbours): codes and scales exactly as gk_fp8_act_quant_bf16 would write
+ * (no reference op; saves the bf16 round trip of the products): codes and scales exactly as gk_fp8_act_quant_bf16 would write
  * for the bf16 output of gk_silu_and_mul_bf16 (q [G][m_pad][128], sa
  * [G][m_pad], G = ceil(width/128); flags GK_FLAG_NATIVE_HALF,
- * GK_FLAG_DECODE_LAYOUT with m_pad = 16). */
+ * GK_FLAG_DECODE_LAYOUT with m_pad = 16, 32 or 64 as there). */
 gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* q,
                                      float* sa, int64_t m_pad, uint32_t flags, void* stream);
 
-/* ---- block-FP8 MoE layer (BASELINE config 5) ------------------------------------
+/* ---- block-FP8 MoE layer (BASELINE.json config 5) ------------------------------------
  * No reference function: the reference has no MoE code for this path.  The
  * layer is build-defined from the reference's pieces (oracle/moe.py restates
  * it on the CPU): top-k (k = 1 or 2) experts per token by router logit, ties

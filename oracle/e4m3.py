@@ -6,8 +6,9 @@ module restates that cast with integer bit operations so that the oracle does
 not depend on one library routine alone; tests/test_oracle_e4m3.py pins it
 against torch's cast on every tie, every code value and a dense random sweep.
 
-Encoding facts (OCP E4M3FN; tests/test_fp8_codec.py:8-12
-of the reference for the magnitude decode):
+Encoding facts (OCP E4M3FN as published in the OCP 8-bit floating point
+specification; tests/test_fp8_codec.py:8-12 of the reference for the magnitude
+decode):
   magnitude m = code & 0x7f, e = m >> 3, f = m & 7
   value = (1 + f/8) * 2**(e-7) for e > 0, f * 2**-9 for e == 0
   0x7f / 0xff are NaN; there is no infinity; max finite is 448 (0x7e).

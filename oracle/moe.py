@@ -1,9 +1,8 @@
 """CPU restatement of the block-FP8 MoE layer (test infrastructure only).
 
-The reference has no MoE, routing or gather/scatter code for the block-FP8 path
-(SURVEY: "no MoE, routing, gather/scatter or collective code exists").  The
-layer of BASELINE config 5 is therefore build-defined, from the reference's own
-pieces:
+The reference has no MoE, routing, gather/scatter or collective code for the
+block-FP8 path.  The MoE layer benchmarked here is therefore build-defined, from
+the reference's own pieces:
 
   route    top-k (k = 1 or 2) experts per token by router logit; ties go to the
            lower expert index.  Combine weights = softmax over the k selected

@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configurations (test infrastructure only).
+"""Seeded synthetic inputs for the BASELINE.json configurations (test infrastructure only).
 
 The reference ships no generator for the block-FP8 path; these follow the
 build-side recipe for BASELINE.json's configs:
@@ -51,7 +51,7 @@ def activations(m, k, seed, *, outlier_frac=0.01, device="cpu"):
 
 
 def config1():
-    """BASELINE config 1: W seed 0, N(0, 0.02), D = 240; X N(0, 1) seed 1, M=4, N=K=256."""
+    """BASELINE.json config 1: W seed 0, N(0, 0.02), D = 240; X N(0, 1) seed 1, M=4, N=K=256."""
     gen = torch.Generator().manual_seed(0)
     w = torch.randn(256, 256, generator=gen) * 0.02
     wq, s = quantize_weight(w, 240.0)

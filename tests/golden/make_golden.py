@@ -82,7 +82,7 @@ def main():
             case[key] = hexs(torch.cat(ys, 0).view(torch.int16))
         cases.append(case)
 
-    # BASELINE config 1 (CPU plumbing): W seed 0 N(0, 0.02), D = 240, X N(0,1), M=4, N=K=256.
+    # BASELINE.json config 1 (CPU plumbing): W seed 0 N(0, 0.02), D = 240, X N(0,1), M=4, N=K=256.
     add("config1", 4, 256, 256, dmax=240.0, codes_from_seed0=True)
     add("ragged_nk", 3, 200, 333, bias=True)
     add("zero_group_tiny_row", 2, 128, 384, zero_group=True, tiny_row=True)

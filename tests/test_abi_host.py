@@ -56,7 +56,11 @@ def test_plan_dispatch_by_m():
         v, mp, ws = ops.plan(m, 6144, 4096)
         # quantized-activation scratch: 16 x 4096 codes + 16 x 32 scales
         assert v == nat.GK_VARIANT_DECODE and mp == 16 and ws == 16 * 4096 + 16 * 32 * 4
-    v, mp, ws = ops.plan(17, 6144, 4096)
+    for m, want_pad in ((17, 32), (32, 32), (33, 64), (64, 64)):
+        v, mp, ws = ops.plan(m, 6144, 4096)
+        # one to four 16-token tiles share each weight fragment
+        assert v == nat.GK_VARIANT_DECODE and mp == want_pad and ws == want_pad * 4096 + want_pad * 32 * 4
+    v, mp, ws = ops.plan(65, 6144, 4096)
     assert v == nat.GK_VARIANT_PREFILL and mp == 256
     v, mp, _ = ops.plan(4096, 7168, 7168)
     assert v == nat.GK_VARIANT_PREFILL and mp == 4096
@@ -77,7 +81,7 @@ def test_plan_rejections():
     assert lib.gk_fp8_block_gemm_plan(4, 256, 256, 1 << 10, p, None, None, None) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
     both = nat.GK_FLAG_FORCE_DECODE | nat.GK_FLAG_FORCE_PREFILL
     assert lib.gk_fp8_block_gemm_plan(4, 256, 256, both, p, None, None, None) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
-    assert lib.gk_fp8_block_gemm_plan(17, 256, 256, nat.GK_FLAG_FORCE_DECODE, p, None, None, None) == \
+    assert lib.gk_fp8_block_gemm_plan(65, 256, 256, nat.GK_FLAG_FORCE_DECODE, p, None, None, None) == \
         nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
     # misaligned weights cannot take the tiled variants
     assert lib.gk_fp8_block_gemm_plan(4, 256, 256, nat.GK_FLAG_FORCE_DECODE, ctypes.c_void_p(257), None, None,

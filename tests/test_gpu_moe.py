@@ -4,7 +4,7 @@ Routing and the expert-sorted row layout are integer/index work: ids,
 row_token, row_of and offsets must be bit-exact; the two softmax weights are
 fp32 and within a few ulp (the device exp).  The layer output must meet the GEMM
 gate (max|y - ref| <= 1e-2 max|ref|, sum|y - ref| / sum|ref| <= 2e-3) at
-small sizes in full and at BASELINE config 5 (512 tokens, 8 experts, top-2,
+small sizes in full and at BASELINE.json config 5 (512 tokens, 8 experts, top-2,
 H=4096, I=14336) stage by stage on sampled tokens and end to end within the
 chain bound below, plus the size-independent property that
 permuting tokens permutes the output bit-for-bit (every row's arithmetic is

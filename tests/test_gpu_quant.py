@@ -52,25 +52,28 @@ def test_strided_rows():
     assert torch.equal(q.permute(1, 0, 2).reshape(8, 1024).cpu(), want_q) and torch.equal(sa.t().cpu(), want_sa)
 
 
-@pytest.mark.parametrize("m,k", [(1, 4096), (5, 333), (16, 14336), (16, 128)])
+@pytest.mark.parametrize("m,k", [(1, 4096), (5, 333), (16, 14336), (16, 128), (17, 1024), (33, 384), (64, 256)])
 @pytest.mark.parametrize("native_half", [False, True])
 def test_act_quant_decode_layout(m, k, native_half):
     """The decode fragment layout holds the same codes as the standard layout, placed as include/gk_fp8.h says:
-    piece (h, l) of group g at byte g*2048 + h*1024 + 16 l = bytes [32 (l // 16) + 16 h, +16) of row l % 16."""
+    block (group g, token tile t) at (g * m_pad/16 + t) * 2048, piece (h, l) at + h*1024 + 16 l = bytes
+    [32 (l // 16) + 16 h, +16) of row 16 t + l % 16; m_pad = 16, 32 or 64 by M."""
     x = make_x(m, k, m * 7 + k, "outliers").cuda()
     qp, sap = ops.act_quant(x, native_half=native_half, decode_layout=True)
-    qs, sas = ops.act_quant(x, native_half=native_half, m_pad=16)
-    assert qp.shape == qs.shape == ((k + 127) // 128, 16, 128)
+    m_pad = 16 * ops.decode_tiles(m)
+    qs, sas = ops.act_quant(x, native_half=native_half, m_pad=m_pad)
+    assert qp.shape == qs.shape == ((k + 127) // 128, m_pad, 128)
     assert torch.equal(sap.cpu().view(torch.int32), sas.cpu().view(torch.int32))
     flat_p = qp.reshape(-1).cpu()
     std = qs.cpu()
-    g_n = std.shape[0]
+    g_n, tiles = std.shape[0], m_pad // 16
     for g in range(g_n):
-        for h in range(2):
-            for lane in range(64):
-                row, quad = lane % 16, lane // 16
-                at = g * 2048 + h * 1024 + 16 * lane
-                assert torch.equal(flat_p[at:at + 16], std[g, row, 32 * quad + 16 * h: 32 * quad + 16 * h + 16])
+        for t in range(tiles):
+            for h in range(2):
+                for lane in range(64):
+                    row, quad = 16 * t + lane % 16, lane // 16
+                    at = (g * tiles + t) * 2048 + h * 1024 + 16 * lane
+                    assert torch.equal(flat_p[at:at + 16], std[g, row, 32 * quad + 16 * h: 32 * quad + 16 * h + 16])
     assert torch.equal(ops.decode_layout_to_standard(qp).cpu(), std)
     want_q, _ = block_fp8.act_quant(x.cpu(), native_half)
-    assert torch.equal(std.permute(1, 0, 2).reshape(16, -1)[:m], want_q)
+    assert torch.equal(std.permute(1, 0, 2).reshape(m_pad, -1)[:m], want_q)

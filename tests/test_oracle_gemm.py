@@ -117,7 +117,7 @@ def test_rejections():
 
 
 def test_config1_plumbing():
-    """BASELINE config 1 through the oracle (the CPU-runnable case)."""
+    """BASELINE.json config 1 through the oracle (the CPU-runnable case)."""
     x, w, s = synth.config1()
     assert int((w.view(torch.uint8) & 0x7F).max()) <= 0x77  # D = 240 keeps codes in the shared range
     y = block_fp8.reference(x, w, s)
