@@ -142,7 +142,9 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
   p->q_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 128);
   p->sa_bytes = align256(static_cast<size_t>(p->m_pad) * static_cast<size_t>(g) * 4);
   if (variant == GK_VARIANT_DECODE)
-    p->dec = gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g), wpack, gk::decode_tiles(m));
+    p->dec = gk::fit_group_step(
+        gk::plan_decode_shape(static_cast<int>(n), static_cast<int>(g), wpack, gk::decode_tiles(m)),
+        static_cast<int>(g));
   // The prefill variant (256 x 256 kernel) addresses its panels with 32-bit
   // offsets: larger shapes run the generic variant (packed weights: rejected).
   if (variant == GK_VARIANT_PREFILL && (p->m_pad * g * 128 > int64_t{0xffffffff} || 256 * k > int64_t{0xffffffff})) {
@@ -158,13 +160,16 @@ gk_status make_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void*
 // Decode GEMM with the quantizer fused: every workgroup quantizes the
 // ceil(M/4) token rows of 4 it needs over its K range.  That redundant work,
 // relative to one workgroup per CU over K = 4096 with all 16 rows, is
-// (workgroups / 256) * (K / 4096) * ceil(M/4) / 4; measured on MI355X, fusing
-// beats the separate quantizer launch while it stays <= 0.4 (config 2 at
-// M <= 8; never the 28672 x 4096 or 4096 x 14336 shapes).
+// (workgroups / 256) * (K / 4096) * ceil(M/4) / 4.  Measured on MI355X with
+// the fused kernel's own load step (fused_quant_shape) over eight N x K
+// shapes and M = 1..16, fusing saves up to 2 us (the separate quantizer
+// launch) while this stays <= 1.2 -- N = 6144, K = 4096 at every M <= 16,
+// 7168 x 7168 at M <= 12, 28672 x 4096 and 4096 x 14336 at M <= 4 -- and
+// costs up to 6 us beyond it.  Near the bound either choice is within 1 us.
 bool fused_quant_pays(int64_t m, int64_t n, int64_t k, const gk::DecodeShape& d) {
   const double wgs = static_cast<double>((n + 16 * d.r - 1) / (16 * d.r));
   const double rows4 = static_cast<double>((std::min<int64_t>(m, 16) + 3) / 4);
-  return (wgs / 256.0) * (static_cast<double>(k) / 4096.0) * (rows4 / 4.0) <= 0.4;
+  return (wgs / 256.0) * (static_cast<double>(k) / 4096.0) * (rows4 / 4.0) <= 1.2;
 }
 
 gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* scales, int64_t scale_rows,
@@ -355,9 +360,12 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
   // quantization work: the GEMM quantizes x itself (one launch, the same
   // codes and scales as the quantizer below).
   if (p.variant == GK_VARIANT_DECODE && p.dec.mt == 1 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
-      ldx % 8 == 0 && fused_quant_pays(m, n, k, p.dec))
-    return run_gemm(p, static_cast<const uint8_t*>(x), nullptr, m, k, w, n, scales, bias, y, ldy, flags, false, s,
-                    ldx);
+      ldx % 8 == 0 && fused_quant_pays(m, n, k, p.dec)) {
+    Plan fused = p;
+    fused.dec = gk::fused_quant_shape(p.dec, static_cast<int>((k + 127) / 128));
+    return run_gemm(fused, static_cast<const uint8_t*>(x), nullptr, m, k, w, n, scales, bias, y, ldy, flags, false,
+                    s, ldx);
+  }
   uint8_t* q = static_cast<uint8_t*>(workspace);
   float* sa = reinterpret_cast<float*>(q + p.q_bytes);
   // The decode variant takes its activations in the packed fragment layout.

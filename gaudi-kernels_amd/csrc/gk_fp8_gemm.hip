@@ -158,11 +158,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
     float sv[U][MT], wv[U];
     if (XQ) {  // activations first: they are needed before the weights
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t go = static_cast<int64_t>(min(g0 + u, gend - 1)) * 256;  // 128 bf16
+      for (int j = 0; j < 4; ++j) {
+        if (j >= xjn) continue;  // wave-uniform: token rows 4j.. are all >= M
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (j < xjn) xb[u][j] = *reinterpret_cast<const uint4*>(xrow[j] + go);
+        for (int u = 0; u < U; ++u)
+          xb[u][j] = *reinterpret_cast<const uint4*>(xrow[j] + static_cast<int64_t>(min(g0 + u, gend - 1)) * 256);
       }
     }
 #pragma unroll
@@ -194,15 +194,18 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
     v8i bq[XQ ? U : 1];  // XQ implies MT == 1
     if (XQ) {
       uint8_t* xq = xqbuf[wave][0];
+      // One straight-line block per token quad j holds the U independent
+      // quantizer chains of the step, which the scheduler interleaves.  All
+      // 16 lanes of a token-group store its (equal) scale.
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+      for (int j = 0; j < 4; ++j) {
+        if (j >= xjn) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (j >= xjn) continue;  // wave-uniform: token rows 4j.. are all >= M
+        for (int u = 0; u < U; ++u) {
           float sc;
           const uint2 c = quant_group8(xb[u][j], true, HALF, &sc);
           *reinterpret_cast<uint2*>(xq + u * (2048 + 64) + xwoff[j]) = c;
-          if ((lane & 15) == 0) *reinterpret_cast<float*>(xq + u * (2048 + 64) + 2048 + 4 * (4 * j + (lane >> 4))) = sc;
+          *reinterpret_cast<float*>(xq + u * (2048 + 64) + 2048 + 4 * (4 * j + (lane >> 4))) = sc;
         }
       }
 #pragma unroll
@@ -345,6 +348,30 @@ DecodeShape plan_decode_shape(int N, int G, bool packed_weights, int mt) {
   return d;
 }
 
+DecodeShape fit_group_step(DecodeShape d, int G) {
+  // A wave's last load step is padded with repeats of its last group (loaded
+  // again, multiplied, and scaled by zero), so U is halved until it divides
+  // every wave's group count (G/NW rounded either way).  Measured on MI355X:
+  // 7168 x 7168 (7 groups a wave) 10.9 -> 10.0 us at M = 16 with U = 1,
+  // 8192 x 2048 (2 a wave) 6.5 -> 5.0 us with U = 2.  NW, and so the result
+  // bits, is unchanged.
+  const int lo = G / d.nw, hi = (G + d.nw - 1) / d.nw;
+  while (d.u > 1 && (lo == 0 || lo % d.u != 0 || hi % d.u != 0)) d.u /= 2;
+  return d;
+}
+
+DecodeShape fused_quant_shape(DecodeShape d, int G) {
+  // With the quantizer fused, a load step also quantizes its U groups, and a
+  // padded step repeats that work for nothing.  U divides every wave's group
+  // count: 4 only where each wave has exactly 4 groups, else 2 where both
+  // counts are even, else 1.  More, shorter steps also keep the quantizer's
+  // arithmetic beside the weight fetch.  Measured on MI355X at M = 1, 8, 16
+  // for nine N x K shapes; NW (and so the result bits) is unchanged.
+  const int lo = G / d.nw, hi = (G + d.nw - 1) / d.nw;
+  d.u = (lo == 4 && hi == 4 && d.u == 4) ? 4 : (lo % 2 == 0 && hi % 2 == 0 && lo > 0) ? 2 : 1;
+  return d;
+}
+
 template <int NW, int R, int U, int MT>
 static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
   static_assert(MT == 1, "the per-channel decode takes one token tile");
@@ -354,9 +381,11 @@ static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Instantiated decode shapes (NW, R, U, MT); plan_decode_shape returns only these.
+// Instantiated decode shapes (NW, R, U, MT); plan_decode_shape and
+// fused_quant_shape return only these (the per-channel decode: the first list).
 #define GK_DECODE_SHAPES1(X) X(2, 2, 4, 1) X(8, 2, 2, 1) X(8, 2, 4, 1) X(8, 1, 2, 1) X(16, 1, 2, 1)
 #define GK_DECODE_SHAPES(X) GK_DECODE_SHAPES1(X)                                               \
+  X(2, 2, 2, 1) X(2, 2, 1, 1) X(8, 2, 1, 1) X(8, 1, 1, 1) X(16, 1, 1, 1)                       \
   X(2, 2, 2, 2) X(8, 2, 1, 2) X(8, 2, 2, 2) X(8, 1, 1, 2) X(16, 1, 1, 2)                       \
   X(2, 2, 1, 4) X(8, 2, 1, 4) X(8, 1, 1, 4) X(16, 1, 1, 4)
 constexpr int decode_key(int nw, int r, int u, int mt) { return ((nw * 10 + r) * 10 + u) * 10 + mt; }

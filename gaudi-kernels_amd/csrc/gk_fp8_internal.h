@@ -26,27 +26,33 @@ __host__ __device__ inline int64_t decode_layout_offset(int g, int64_t row, int 
 }
 constexpr int kPrefillRowTile = 256; // prefill variant: M padded to the token tile
 
-// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in VALU
-// data-parallel moves: xor 1 and xor 2 (quad_perm), then the half-row and
-// row mirrors pair quads 0-1 / 2-3 and the two halves.  Lanes whose source is
-// inactive keep their own value.  The maximum does not depend on the order.
+// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15) of
+// non-negative floats, in VALU data-parallel moves: xor 1 and xor 2
+// (quad_perm), then the half-row and row mirrors pair quads 0-1 / 2-3 and the
+// two halves.  Non-negative floats order as their bit patterns, so each step
+// is one unsigned max with a DPP operand (v_max_u32_dpp: no separate move and
+// no NaN canonicalization, which an fmaxf on a moved value costs).  An
+// inactive source lane reads as 0 (bound_ctrl), the identity of the maximum.
+// The maximum does not depend on the order.  Returns the bit pattern.
 template <int CTRL>
-__device__ inline float dpp_fmax(float v) {
-  const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xf, 0xf, false);
-  return fmaxf(v, __int_as_float(o));
+__device__ inline uint32_t dpp_umax(uint32_t v) {
+  const uint32_t o =
+      static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, true));
+  return v > o ? v : o;
 }
-__device__ inline float row_max16(float v) {
-  v = dpp_fmax<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = dpp_fmax<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = dpp_fmax<0x141>(v);  // row_half_mirror
-  return dpp_fmax<0x140>(v);  // row_mirror
+__device__ inline uint32_t row_max16_bits(float v) {  // v >= +0
+  uint32_t b = __float_as_uint(v);
+  b = dpp_umax<0xB1>(b);   // quad_perm [1,0,3,2]
+  b = dpp_umax<0x4E>(b);   // quad_perm [2,3,0,1]
+  b = dpp_umax<0x141>(b);  // row_half_mirror
+  return dpp_umax<0x140>(b);  // row_mirror
 }
 
 // ---- 1x128 activation quantizer (block_fp8_oracle.py:25-28, :32,:34) -------
 // Sixteen consecutive lanes own one 128-element group, 8 bf16 each (one
 // 16-byte load).  Returns the lane's 8 OCP E4M3 codes (byte i = element i)
 // and writes the group's scale (x2 in native_half mode).  amax is reduced
-// over the 16 lanes (one DPP row, row_max16); the fp32 quotient is act_quotient
+// over the 16 lanes (one DPP row, row_max16_bits); the fp32 quotient is act_quotient
 // (exact E4M3 codes of the IEEE quotient); the encode is the gfx950
 // v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN), which equals
 // e4m3_rne for every |v| <= 464 -- and |x / s| < 464 always holds because
@@ -62,9 +68,13 @@ __device__ inline uint2 quant_group8(uint4 raw, bool live, bool half, float* sca
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = row_max16(amax);
-  const float s = act_scale(amax);
-  const float r = 1.0f / s;  // IEEE division, once per lane
+  // act_scale(amax) with the 1e-10 floor taken on the bit pattern (amax >= +0)
+  const uint32_t amax_bits = row_max16_bits(amax);
+  const float s = __uint_as_float(max(amax_bits, __float_as_uint(1e-10f))) * (1.0f / 448.0f);
+  // 1/s: the hardware reciprocal (1 ulp) refined by one Newton step, which
+  // leaves r within one ulp of fp32(1/s); act_quotient is exact for any such r
+  const float r0 = __builtin_amdgcn_rcpf(s);
+  const float r = fmaf(fmaf(-s, r0, 1.0f), r0, r0);
   float q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) q[i] = act_quotient(v[i], s, r);
@@ -104,6 +114,10 @@ struct DecodeShape {
   int nw, r, u, mt;  // mt: 16-token column tiles
 };
 DecodeShape plan_decode_shape(int N, int G, bool packed_weights, int mt);
+// U reduced to divide every wave's group count (no padded load steps).
+DecodeShape fit_group_step(DecodeShape d, int G);
+// The shape of the decode kernel with the quantizer fused (XQ, one token tile).
+DecodeShape fused_quant_shape(DecodeShape d, int G);
 
 // Quantized activations qa [G][Mpad][128] / sa [G][Mpad] (launch_act_quant)
 // times weight codes w [N, K] with block scales sw [ceil(N/128), G].

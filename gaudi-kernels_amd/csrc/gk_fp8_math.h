@@ -59,17 +59,19 @@ __host__ __device__ inline uint32_t e4m3_rne(float v) {
 // fp32(max(amax, 1e-10)) * fp32(1/448), one fp32 multiply.
 __host__ __device__ inline float act_scale(float amax) { return fmaxf(amax, 1e-10f) * (1.0f / 448.0f); }
 
-// fp32 quotient x / s for the activation quantizer, given r = fp32(1 / s)
-// (one IEEE division per group).  q0 = x*r is refined by one residual step,
-// q = q0 + fma(-s, q0, x) * r, and the sign of x is reapplied (the residual
-// step turns -0 into +0).  For every finite bf16 x and every scale s =
+// fp32 quotient x / s for the activation quantizer, given r within one ulp of
+// fp32(1 / s).  q0 = x*r is refined by one residual step,
+// q = q0 + (x - s*q0) * r, computed as fma(-fma(s, q0, -x), r, q0): the
+// residual is formed with the opposite sign and negated, which keeps -0 for
+// x = -0 (fma(-s, q0, x) would give +0 there) and costs only source
+// negations.  For every finite bf16 x and every scale s =
 // act_scale(a) over all bf16 magnitudes a >= |x|, e4m3_rne(q) equals
 // e4m3_rne(x / s) with IEEE division; the only quotients that differ are
 // fp32 subnormals, which encode to zero either way.  The exhaustive check
 // is tests/csrc/math_check.cpp:mc_div_mismatches.
 __host__ __device__ inline float act_quotient(float x, float s, float r) {
   const float q0 = x * r;
-  return copysignf(fmaf(fmaf(-s, q0, x), r, q0), x);
+  return fmaf(-fmaf(s, q0, -x), r, q0);
 }
 
 // OCP E4M3FN code -> fp32 value (finite codes; 0x7f decodes to 480, never used).

@@ -1,6 +1,7 @@
 // Host build of gaudi-kernels_amd/csrc/gk_fp8_math.h (the arithmetic the
 // gfx950 kernels run), exposed with a C ABI so tests can sweep it against
 // the CPU oracle.  Built by tests/test_math_host.py with g++.
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -14,20 +15,25 @@ namespace {
 float bf16_bits_to_f32(uint32_t h) { return gk::bits_f32(h << 16); }
 
 // Mismatching e4m3 codes between gk::act_quotient and IEEE division, for
-// amax over the bf16 magnitudes amax_lo <= a < amax_hi (step `step`) and
-// every finite bf16 x with |x| <= a.
+// amax over the bf16 magnitudes amax_lo <= a < amax_hi (step `step`), every
+// finite bf16 x with |x| <= a and every reciprocal r within one ulp of
+// fp32(1/s).
 int64_t div_mismatches_range(uint32_t a_first, uint32_t a_step, uint32_t a_end) {
   int64_t bad = 0;
   for (uint32_t ah = a_first; ah < a_end; ah += a_step) {
     const float s = gk::act_scale(bf16_bits_to_f32(ah));
     volatile float one = 1.0f;
-    const float r = one / s;
+    const float rn = one / s;
+    // the correctly rounded reciprocal and its two neighbours: any r within
+    // one ulp of fp32(1/s), which covers every faithful reciprocal
+    const float rs[3] = {nextafterf(rn, 0.0f), rn, nextafterf(rn, INFINITY)};
     for (uint32_t xh = 0; xh < 0x10000u; ++xh) {
       if ((xh & 0x7fffu) > ah) continue;
       const float x = bf16_bits_to_f32(xh);
       volatile float vx = x;
-      const float ieee = vx / s;
-      if (gk::e4m3_rne(gk::act_quotient(x, s, r)) != gk::e4m3_rne(ieee)) ++bad;
+      const uint32_t want = gk::e4m3_rne(vx / s);
+      for (float r : rs)
+        if (gk::e4m3_rne(gk::act_quotient(x, s, r)) != want) ++bad;
     }
   }
   return bad;

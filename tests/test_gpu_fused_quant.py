@@ -1,7 +1,8 @@
 """Decode GEMM with the 1x128 quantizer fused into its activation load (gk_fp8_block_gemm_bf16, M <= 16).
 
-The op fuses the quantizer where its redundant per-workgroup work is small (config 2 at M <= 8,
-small shapes at every M) and runs the standalone quantizer otherwise.  Either way it must equal
+The op fuses the quantizer where its redundant per-workgroup work is small (N = 6144, K = 4096
+at every M <= 16; 7168 x 7168 at M <= 12; 28672 x 4096 and 4096 x 14336 at M <= 4; small shapes
+at every M) and runs the standalone quantizer otherwise.  Either way it must equal
 act_quant followed by the GEMM on the quantized activations bit for bit (same codes, same scales,
 same accumulation order), for row-major and packed weights, both modes, with bias, M values that
 leave 1-3 clamped rows in a row quad, padded row strides, and activations that are not 16-byte
@@ -22,7 +23,9 @@ def unfused(x, w, s, bias, native_half):
     return ops.block_fp8_gemm_q(q, sa, x.shape[0], w, s, bias, native_half=native_half, decode_layout=True)
 
 
-@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336), (28672, 4096), (1000, 384), (24, 128)])
+# every fused load step: (NW, R, U) = (8, 2, 4), (8, 1, 2), (2, 2, 2), (16, 1, 1), (8, 2, 1), (8, 1, 1)
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336), (28672, 4096), (1000, 384), (24, 128), (7168, 7168),
+                                 (4096, 7168)])
 @pytest.mark.parametrize("native_half", [False, True])
 def test_fused_equals_quant_then_gemm(n, k, native_half):
     w, s = synth.weight(n, k, seed=n + k)
@@ -32,6 +35,7 @@ def test_fused_equals_quant_then_gemm(n, k, native_half):
     for m in (1, 3, 5, 8, 16):
         x = synth.activations(m, k, seed=m).cuda()
         x[0, :128] = 0.0                       # an all-zero group
+        x[-1, 130:140] = -0.0                  # negative zeros in a live group (code 0x80)
         if m > 1:
             x[1, 128:256] *= 1e-30             # a tiny group
         for weight in (w, p):

@@ -23,6 +23,7 @@ def make_x(m, k, seed, kind):
             x[2] *= 1e30                             # huge row
         if m > 3:
             x[3, ::7] = 0
+            x[3, 3::7] = -0.0                        # negative zeros encode to 0x80
     return x.bfloat16()
 
 

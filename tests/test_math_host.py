@@ -115,6 +115,7 @@ def test_swar_codec_all_bytes_all_lanes(mc):
 
 
 def test_quantizer_division_exhaustive(mc):
-    """gk::act_quotient gives the IEEE-division E4M3 code for every bf16 x and bf16 amax >= |x| (2^31 pairs)."""
+    """gk::act_quotient gives the IEEE-division E4M3 code for every bf16 x and bf16 amax >= |x| (2^31 pairs), with
+    the correctly rounded reciprocal of the scale and with either of its neighbours (any faithful reciprocal)."""
     mc.mc_div_mismatches.restype = ctypes.c_int64
     assert mc.mc_div_mismatches(ctypes.c_int(min(8, os.cpu_count() or 1))) == 0
