@@ -1,6 +1,6 @@
 """Benchmark of the MI355X block-FP8 W8A8 GEMM (BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|prefill|mlp|moe]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|qkv|prefill|mlp|moe]
 
 Workload (one "step"): BASELINE.json configs[1] decode sweep -- one block-FP8
 GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
@@ -210,7 +210,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["decode", "prefill", "mlp", "moe"], default=None)
+    ap.add_argument("--only", choices=["decode", "qkv", "prefill", "mlp", "moe"], default=None)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print per-kernel, per-grid tables of a rocprofv3 csv output directory and exit")
     args = ap.parse_args()
@@ -320,6 +320,37 @@ def main():
                           "m16": {"achieved": round(gemm_bytes(16, n, k) / (launch_us[-1] * 1e-6) / 1e9, 1),
                                   "launch_us": round(launch_us[-1], 3)}}
     result["decode_sweep"] = per_m
+
+    # ---- config 2 as a layer step: fused add + RMSNorm feeding the QKV GEMM --------------------------
+    # (a) one norm kernel that also writes the 1x128 codes in the decode layout, then the GEMM on them;
+    # (b) the reference's op split: fused add + RMSNorm to bf16, then the GEMM op (quantizer fused).
+    if args.only in (None, "qkv"):
+        w, s = synth.weight(n, k, seed=2000)
+        rot = Rotation(w, s, packed=True)
+        gamma = (torch.rand(k, generator=torch.Generator().manual_seed(2100)) + 0.5).bfloat16().cuda()
+        chain = {}
+        for m in ms_list:
+            xm = synth.activations(m, k, seed=2200 + m).cuda()
+            rm = synth.activations(m, k, seed=2300 + m).cuda()
+            om = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+
+            def fused_chain():
+                q, sa, _ = ops.rms_norm_quant(xm, gamma, 1e-6, residual=rm, decode_layout=True)
+                ops.block_fp8_gemm_q(q, sa, m, *rot.next(), out=om, decode_layout=True)
+
+            def split_chain():
+                _, h = ops.fused_add_rms_norm(xm, rm, gamma, 1e-6)
+                ops.block_fp8_gemm(h, *rot.next(), out=om, workspace=wss[m])
+
+            t_norm = time_loop(lambda: ops.rms_norm_quant(xm, gamma, 1e-6, residual=rm, decode_layout=True), 100, 10)
+            t_fused = time_loop(fused_chain, 100, 10)
+            t_split = time_loop(split_chain, 100, 10)
+            chain[str(m)] = {"norm_quant_us": round(t_norm * 1e3, 2), "fused_chain_us": round(t_fused * 1e3, 2),
+                             "split_chain_us": round(t_split * 1e3, 2)}
+        result["qkv_chain"] = chain
+        log(f"[bench] qkv chain (fused add + RMSNorm -> QKV GEMM): {chain}")
+        del rot
+        torch.cuda.empty_cache()
 
     # ---- config 3: MLP pair decode at M=16 ------------------------------------------------------
     if args.only in (None, "mlp"):

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstring>
 #include <mutex>
 
@@ -36,6 +37,9 @@ constexpr const char* kOps[] = {
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
     "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (build-defined)
     "gk_fp8_pack_weight_v1",        // load-time layout packing (fp8_codec.py:19 "a separate step")
+    "gk_rms_norm_bf16_v1",          // rms_norm_bf16.c, glue generic_dense_glue.cpp:135-190
+    "gk_fused_add_rms_norm_bf16_v1",  // fused_add_rms_norm_bf16.c, same glue
+    "gk_fp8_rms_norm_quant_bf16_v1",  // (fused add +) RMSNorm fused with the 1x128 quantizer (build-defined)
 };
 constexpr uint32_t kNumOps = sizeof(kOps) / sizeof(kOps[0]);
 
@@ -513,6 +517,83 @@ gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t 
                                                 static_cast<int>(width), static_cast<int>(m_pad),
                                                 static_cast<uint8_t*>(q), sa, (flags & GK_FLAG_NATIVE_HALF) != 0,
                                                 packed, static_cast<hipStream_t>(stream)));
+}
+
+// ---- RMSNorm ----------------------------------------------------------------------------
+namespace {
+
+// generic_dense_glue.cpp:146-160: epsilon finite and > 0 and weight_offset
+// finite (else the layer configuration is unsupported), then 1 <= width <=
+// 8192 and rows >= 1 (input size), then bf16 (2-byte aligned) tensors.
+gk_status check_norm(const void* x, int64_t rows, int64_t width, int64_t ld_in, const void* gamma, float eps,
+                     float off) {
+  if (!x || !gamma) return GK_INVALID_ARGUMENT;
+  if (!std::isfinite(eps) || eps <= 0.0f || !std::isfinite(off)) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (rows < 1 || rows > kMaxDim || width < 1 || width > gk::kNormMaxWidth || ld_in < width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gamma)) & 1) return GK_INCOMPATIBLE_DATA_TYPE;
+  return GK_SUCCESS;
+}
+
+bool odd(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1) != 0; }
+
+}  // namespace
+
+gk_status gk_rms_norm_bf16(const void* x, int64_t rows, int64_t width, int64_t ld_in, const void* gamma,
+                           float epsilon, float weight_offset, void* out, int64_t ld_out, void* stream) {
+  gk_status st = check_norm(x, rows, width, ld_in, gamma, epsilon, weight_offset);
+  if (st != GK_SUCCESS) return st;
+  if (!out) return GK_INVALID_ARGUMENT;
+  if (ld_out < width) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (odd(out)) return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_rms_norm(static_cast<const uint16_t*>(x), nullptr, ld_in,
+                                      static_cast<const uint16_t*>(gamma), static_cast<int>(rows),
+                                      static_cast<int>(width), epsilon, weight_offset, nullptr,
+                                      static_cast<uint16_t*>(out), ld_out, nullptr, nullptr, 0, false, false,
+                                      static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fused_add_rms_norm_bf16(const void* x, const void* residual, int64_t rows, int64_t width,
+                                     int64_t ld_in, const void* gamma, float epsilon, float weight_offset,
+                                     void* residual_out, void* norm_out, int64_t ld_out, void* stream) {
+  gk_status st = check_norm(x, rows, width, ld_in, gamma, epsilon, weight_offset);
+  if (st != GK_SUCCESS) return st;
+  if (!residual || !residual_out || !norm_out) return GK_INVALID_ARGUMENT;
+  if (ld_out < width) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (odd(residual) || odd(residual_out) || odd(norm_out)) return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_rms_norm(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(residual), ld_in,
+                                      static_cast<const uint16_t*>(gamma), static_cast<int>(rows),
+                                      static_cast<int>(width), epsilon, weight_offset,
+                                      static_cast<uint16_t*>(residual_out), static_cast<uint16_t*>(norm_out), ld_out,
+                                      nullptr, nullptr, 0, false, false, static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_rms_norm_quant_bf16(const void* x, const void* residual, int64_t rows, int64_t width,
+                                     int64_t ld_in, const void* gamma, float epsilon, float weight_offset,
+                                     void* residual_out, int64_t ld_out, void* q, float* sa, int64_t m_pad,
+                                     uint32_t flags, void* stream) {
+  gk_status st = check_norm(x, rows, width, ld_in, gamma, epsilon, weight_offset);
+  if (st != GK_SUCCESS) return st;
+  if (!q || !sa || (residual_out && !residual)) return GK_INVALID_ARGUMENT;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_DECODE_LAYOUT}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
+  if (m_pad < rows || m_pad > kMaxDim || (residual_out && ld_out < width)) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (packed && m_pad != 16 && m_pad != 32 && m_pad != 64) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (odd(residual) || odd(residual_out) || (reinterpret_cast<uintptr_t>(q) & 7) ||
+      (reinterpret_cast<uintptr_t>(sa) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_rms_norm(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(residual), ld_in,
+                                      static_cast<const uint16_t*>(gamma), static_cast<int>(rows),
+                                      static_cast<int>(width), epsilon, weight_offset,
+                                      static_cast<uint16_t*>(residual_out), nullptr, residual_out ? ld_out : 0,
+                                      static_cast<uint8_t*>(q), sa, static_cast<int>(m_pad),
+                                      (flags & GK_FLAG_NATIVE_HALF) != 0, packed, static_cast<hipStream_t>(stream)));
 }
 
 // ---- MoE ------------------------------------------------------------------------------

@@ -108,6 +108,15 @@ hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, h
 hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mpad, uint8_t* q, float* sa,
                             bool half, bool packed, hipStream_t stream);
 
+// RMSNorm of bf16 rows (width <= kNormMaxWidth), optionally fused with a
+// residual add (res != nullptr; residual_out written when res_out != nullptr)
+// and with the 1x128 quantizer (q != nullptr: codes and scales in the layout
+// of launch_act_quant, Mpad rows; norm_out may then be nullptr).
+constexpr int kNormMaxWidth = 8192;  // generic_dense_glue.cpp:153
+hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* res, int64_t ld_in, const uint16_t* gamma, int rows,
+                           int width, float eps, float off, uint16_t* res_out, uint16_t* norm_out, int64_t ld_out,
+                           uint8_t* q, float* sa, int Mpad, bool half, bool packed, hipStream_t stream);
+
 // Decode variant shape: NW waves per workgroup (splitting K), R 16-row weight
 // tiles per workgroup, U groups per load step.  Chosen by plan_decode_shape.
 struct DecodeShape {

@@ -82,6 +82,12 @@ SIGNATURES = {
                                           _c_i64, _c_u32, _c_vp]),
     "gk_silu_and_mul_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]),
     "gk_fp8_silu_mul_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _fp, _c_i64, _c_u32, _c_vp]),
+    "gk_rms_norm_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, ctypes.c_float, ctypes.c_float, _c_vp,
+                                  _c_i64, _c_vp]),
+    "gk_fused_add_rms_norm_bf16": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, ctypes.c_float,
+                                            ctypes.c_float, _c_vp, _c_vp, _c_i64, _c_vp]),
+    "gk_fp8_rms_norm_quant_bf16": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, ctypes.c_float,
+                                            ctypes.c_float, _c_vp, _c_i64, _c_vp, _fp, _c_i64, _c_u32, _c_vp]),
     "gk_fp8_moe_rows_max": (_c_int, [_c_i64, _c_i64, _c_int, ctypes.POINTER(_c_i64)]),
     "gk_fp8_moe_workspace_bytes": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, ctypes.POINTER(_c_size)]),
     "gk_fp8_moe_route": (_c_int, [_fp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _fp, _c_vp, _c_vp, _c_i64, _c_vp,

@@ -339,6 +339,72 @@ def silu_mul_quant(gate_up, *, native_half=False, m_pad=None, decode_layout=Fals
     return q, sa
 
 
+def _check_rows(t, name, device, width=None):
+    if t.dtype != torch.bfloat16 or t.ndim != 2 or t.stride(1) != 1 or t.device != device:
+        raise ValueError(f"{name} must be a 2-D bf16 tensor with unit column stride on the GPU")
+    if width is not None and t.shape[1] != width:
+        raise ValueError(f"{name} must have {width} columns")
+
+
+def _norm_inputs(x, gamma, residual):
+    device = require_device(x.device)
+    _check_rows(x, "x", device)
+    rows, width = x.shape
+    if gamma.dtype != torch.bfloat16 or gamma.shape != (width,) or gamma.stride(0) != 1 or gamma.device != device:
+        raise ValueError("gamma must be a contiguous bf16 [width] tensor on the same GPU")
+    if residual is not None:
+        _check_rows(residual, "residual", device, width)
+        if residual.shape[0] != rows or residual.stride(0) != x.stride(0):
+            raise ValueError("residual must have the shape and row stride of x")
+    return device, rows, width
+
+
+def rms_norm(x, gamma, epsilon=1e-6, weight_offset=0.0, *, out=None):
+    """bf16 [rows, W] -> bf16 [rows, W] = bf16((x * inv) * (gamma + weight_offset)),
+    inv = 1 / sqrt(mean(x^2) + epsilon) per row (gk_rms_norm_bf16_v1)."""
+    device, rows, width = _norm_inputs(x, gamma, None)
+    if out is None:
+        out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    else:
+        _check_rows(out, "out", device, width)
+    nat.check("gk_rms_norm_bf16",
+              nat.load().gk_rms_norm_bf16(_ptr(x), rows, width, x.stride(0), _ptr(gamma), epsilon, weight_offset,
+                                          _ptr(out), out.stride(0), _stream(device)))
+    return out
+
+
+def fused_add_rms_norm(x, residual, gamma, epsilon=1e-6, weight_offset=0.0):
+    """-> (residual_out = bf16(x + residual), norm_out = rms_norm(residual_out)) (gk_fused_add_rms_norm_bf16_v1)."""
+    device, rows, width = _norm_inputs(x, gamma, residual)
+    res_out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    norm_out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    nat.check("gk_fused_add_rms_norm_bf16",
+              nat.load().gk_fused_add_rms_norm_bf16(_ptr(x), _ptr(residual), rows, width, x.stride(0), _ptr(gamma),
+                                                    epsilon, weight_offset, _ptr(res_out), _ptr(norm_out),
+                                                    width, _stream(device)))
+    return res_out, norm_out
+
+
+def rms_norm_quant(x, gamma, epsilon=1e-6, weight_offset=0.0, *, residual=None, native_half=False, m_pad=None,
+                   decode_layout=False):
+    """(Fused add +) RMSNorm fused with the 1x128 quantizer -> (codes [G, m_pad, 128], sa [G, m_pad]) as
+    act_quant of the normalized rows would give, plus residual_out (bf16 [rows, W]) when `residual` is given:
+    (q, sa) or (q, sa, residual_out).  decode_layout as in act_quant."""
+    device, rows, width = _norm_inputs(x, gamma, residual)
+    g = (width + 127) // 128
+    m_pad = (16 * decode_tiles(rows) if decode_layout else rows) if m_pad is None else m_pad
+    q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
+    sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
+    res_out = None if residual is None else torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    flags = (nat.GK_FLAG_NATIVE_HALF if native_half else 0) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
+    nat.check("gk_fp8_rms_norm_quant_bf16",
+              nat.load().gk_fp8_rms_norm_quant_bf16(_ptr(x), None if residual is None else _ptr(residual), rows,
+                                                    width, x.stride(0), _ptr(gamma), epsilon, weight_offset,
+                                                    None if res_out is None else _ptr(res_out), width, _ptr(q),
+                                                    _ptr(sa), m_pad, flags, _stream(device)))
+    return (q, sa) if residual is None else (q, sa, res_out)
+
+
 def moe_rows_max(tokens, n_experts, top_k=2):
     """Padded row count of the expert-sorted layout (an upper bound of the rows in use)."""
     rows = ctypes.c_int64(0)

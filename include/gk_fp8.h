@@ -234,6 +234,41 @@ gk_status gk_silu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width,
 gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* q,
                                      float* sa, int64_t m_pad, uint32_t flags, void* stream);
 
+/* ---- RMSNorm ------------------------------------------------------------------ */
+
+/* The reference's gk_rms_norm_bf16_v1 (csrc/tpc/generic_dense/rms_norm_bf16.c:4-53,
+ * glue csrc/host/generic_dense_glue.cpp:135-190): x bf16 [rows, width] (row
+ * stride ld_in), gamma bf16 [width] -> out bf16 [rows, width] (row stride
+ * ld_out), out = bf16((x * inv) * (gamma + weight_offset)) with
+ * inv = 1 / sqrt(sum(x^2) * (1/width) + epsilon) per row.  The sum of squares
+ * is taken exactly (fp64, fixed order) and rounded to fp32 once; inv is
+ * fp32(1 / sqrt) of the fp32 argument; the products are fp32.  As the glue:
+ * epsilon must be finite and > 0 and weight_offset finite
+ * (GK_UNSUPPORTED_LAYER_CONFIGURATION), 1 <= width <= 8192 and rows >= 1
+ * (GK_INCOMPATIBLE_INPUT_SIZE). */
+gk_status gk_rms_norm_bf16(const void* x, int64_t rows, int64_t width, int64_t ld_in, const void* gamma,
+                           float epsilon, float weight_offset, void* out, int64_t ld_out, void* stream);
+
+/* The reference's gk_fused_add_rms_norm_bf16_v1 (fused_add_rms_norm_bf16.c:4-63,
+ * same glue): residual_out = bf16(x + residual) (fp32 sum, one rounding),
+ * norm_out = gk_rms_norm_bf16 of residual_out.  x and residual share ld_in,
+ * both outputs ld_out. */
+gk_status gk_fused_add_rms_norm_bf16(const void* x, const void* residual, int64_t rows, int64_t width,
+                                     int64_t ld_in, const void* gamma, float epsilon, float weight_offset,
+                                     void* residual_out, void* norm_out, int64_t ld_out, void* stream);
+
+/* The same normalized rows quantized per 1x128 group for the next block-FP8
+ * GEMM (no reference op; the upstream fusion of the activation quantizer into
+ * the norm): codes and scales exactly as gk_fp8_act_quant_bf16 would write for
+ * norm_out (q [G][m_pad][128], sa [G][m_pad], G = ceil(width/128); flags
+ * GK_FLAG_NATIVE_HALF, GK_FLAG_DECODE_LAYOUT with m_pad = 16, 32 or 64).
+ * residual may be NULL (plain RMSNorm); with a residual, residual_out (row
+ * stride ld_out) may be NULL. */
+gk_status gk_fp8_rms_norm_quant_bf16(const void* x, const void* residual, int64_t rows, int64_t width,
+                                     int64_t ld_in, const void* gamma, float epsilon, float weight_offset,
+                                     void* residual_out, int64_t ld_out, void* q, float* sa, int64_t m_pad,
+                                     uint32_t flags, void* stream);
+
 /* ---- block-FP8 MoE layer ------------------------------------
  * No reference function: the reference has no MoE code for this path.  The
  * layer is build-defined from the reference's pieces (oracle/moe.py restates
