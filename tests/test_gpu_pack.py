@@ -1,8 +1,9 @@
 """Load-time weight packing on the GPU (gk_fp8_pack_weight) and the GEMMs on packed weights.
 
 The packed bytes equal oracle/pack.py; every GEMM on packed weights is bit-identical to the
-same GEMM on the row-major codes (decode and 256 x 256 kernels, both modes, bias, ragged N),
-and the row-major GEMM is pinned to the oracle by the golden vectors (test_gpu_gemm.py).
+same GEMM on the row-major codes (the decode kernel at one to four token tiles and the 256 x 256
+kernel, both modes, bias, ragged N), and the row-major GEMM is pinned to the oracle by the golden
+vectors (test_gpu_gemm.py).
 """
 
 import numpy as np
@@ -31,7 +32,8 @@ def test_pack_bytes(n, k):
 
 
 CASES = [(1, 6144, 4096), (5, 1000, 256), (16, 28672, 4096), (16, 4096, 14336), (17, 264, 1024),
-         (100, 1000, 512), (300, 6144, 4096), (600, 520, 384)]
+         (40, 7168, 7168), (64, 6144, 4096), (33, 28672, 512), (100, 1000, 512), (300, 6144, 4096),
+         (600, 520, 384)]
 
 
 @pytest.mark.parametrize("m,n,k", CASES)
@@ -47,8 +49,9 @@ def test_gemm_packed_bit_identical(m, n, k, native_half):
         assert torch.equal(y_row.view(torch.int16), y_pack.view(torch.int16)), (m, n, k, b is None)
 
 
-def test_gemm_q_packed_decode_layout():
-    m, n, k = 16, 6144, 4096
+@pytest.mark.parametrize("m", [16, 32, 64])
+def test_gemm_q_packed_decode_layout(m):
+    n, k = 6144, 4096
     w, s = weights(n, k, 3)
     x = synth.activations(m, k, 3).cuda()
     q, sa = ops.act_quant(x, decode_layout=True)
