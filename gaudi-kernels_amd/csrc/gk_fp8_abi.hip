@@ -679,7 +679,8 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
                           const void* w_dn, const float* s_dn, void* y, int64_t ldy, uint32_t flags,
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (!x || !logits || !w_gu || !s_gu || !w_dn || !s_dn || !y || !workspace) return GK_INVALID_ARGUMENT;
-  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_WEIGHT_PACKED}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  const bool wpack = (flags & GK_FLAG_WEIGHT_PACKED) != 0;
   MoeLayout L;
   gk_status st = moe_layout(T, H, I, E, top_k, &L);
   if (st != GK_SUCCESS) return st;
@@ -710,7 +711,7 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   gk::GemmArgs a{};
   a.qa = q1; a.sa = sa1; a.w = static_cast<const uint8_t*>(w_gu); a.sw = s_gu; a.bias = nullptr;
   a.y = hpre; a.ldy = 2 * I; a.M = R; a.N = static_cast<int>(2 * I); a.K = static_cast<int>(H);
-  a.G = static_cast<int>(H / 128); a.Mpad = R; a.half_w = half;
+  a.G = static_cast<int>(H / 128); a.Mpad = R; a.half_w = half; a.wpack = wpack;
   e = gk::launch_gemm_grouped256(a, r.off, r.cnt, static_cast<int>(E), 1, nullptr, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   uint8_t* q2 = ws + L.q2;
@@ -722,7 +723,7 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   gk::GemmArgs d{};
   d.qa = q2; d.sa = sa2; d.w = static_cast<const uint8_t*>(w_dn); d.sw = s_dn; d.bias = nullptr;
   d.y = nullptr; d.ldy = H; d.M = R; d.N = static_cast<int>(H); d.K = static_cast<int>(I);
-  d.G = static_cast<int>(I / 128); d.Mpad = R; d.half_w = half;
+  d.G = static_cast<int>(I / 128); d.Mpad = R; d.half_w = half; d.wpack = wpack;
   e = gk::launch_gemm_grouped256(d, r.off, r.cnt, static_cast<int>(E), L.kparts, z, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   return from_hip(gk::launch_moe_combine(z, L.kparts, static_cast<int64_t>(R) * H, static_cast<int>(H), r.row_of,

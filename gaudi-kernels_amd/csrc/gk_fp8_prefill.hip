@@ -355,14 +355,21 @@ hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
 }
 
 // Grouped form: a.Mpad = padded rows (multiple of 256), a.M = a.Mpad; weights
-// [n_groups][N][K], scales [n_groups][ceil(N/128)][G]; group_off, group_cnt on device.
+// [n_groups][N][K] (a.wpack: each group's weights packed by launch_pack_weight,
+// one after the other), scales [n_groups][ceil(N/128)][G]; group_off,
+// group_cnt on device.
 hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt,
                                   int n_groups, int kparts, float* yp, hipStream_t stream) {
   if (a.Mpad % kBM != 0 || n_groups < 1 || kparts < 1 || kparts > 2 || (kparts > 1 && !yp) || (yp && a.N % 4) ||
-      !prefill256_fits(a) || a.wpack)
+      !prefill256_fits(a))
     return hipErrorInvalidValue;
-  const int64_t w_stride = static_cast<int64_t>(a.N) * a.K;
+  const int64_t w_stride = a.wpack ? packed_weight_bytes(a.N, a.K) : static_cast<int64_t>(a.N) * a.K;
   const int64_t sw_stride = static_cast<int64_t>((a.N + 127) / 128) * a.G;
+  if (a.wpack)
+    return a.half_w
+               ? launch256<true, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, stream)
+               : launch256<false, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
+                                              stream);
   return a.half_w ? launch256<true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, stream)
                   : launch256<false, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
                                            stream);

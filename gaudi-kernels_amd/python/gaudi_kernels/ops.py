@@ -169,6 +169,38 @@ def pack_weight(weight):
     return PackedWeight(data, n, k)
 
 
+class PackedExperts:
+    """Expert weights [E, n, k] packed one expert after the other (pack_experts) for moe_block_fp8."""
+
+    def __init__(self, data, e, n, k):
+        self.data, self.e, self.n, self.k = data, e, n, k
+
+    @property
+    def shape(self):
+        return (self.e, self.n, self.k)
+
+    @property
+    def device(self):
+        return self.data.device
+
+
+def pack_experts(weights):
+    """Row-major E4M3 expert codes [E, N, K] (K % 128 == 0) on the GPU -> PackedExperts (asynchronous):
+    expert e packed by gk_fp8_pack_weight at byte e * packed_weight_bytes(N, K)."""
+    device = require_device(weights.device)
+    if weights.dtype not in (torch.float8_e4m3fn, torch.uint8) or weights.ndim != 3 or not weights.is_contiguous():
+        raise ValueError("expected contiguous E4M3 expert weights [E, N, K]")
+    e, n, k = weights.shape
+    per = packed_weight_bytes(n, k)
+    data = torch.empty(e * per, dtype=torch.uint8, device=device)
+    lib = nat.load()
+    src = _u8(weights)
+    for i in range(e):
+        nat.check("gk_fp8_pack_weight",
+                  lib.gk_fp8_pack_weight(_ptr(src[i]), n, k, _ptr(data[i * per:]), per, _stream(device)))
+    return PackedExperts(data, e, n, k)
+
+
 def _weight_args(weight):
     """(uint8 tensor passed as w, n, k, extra flags) for a row-major or packed weight."""
     if isinstance(weight, PackedWeight):
@@ -444,6 +476,7 @@ def moe_block_fp8(x, logits, w_gate_up, s_gate_up, w_down, s_down, *, top_k=2, n
 
     x bf16 [T, H]; logits fp32 [T, E]; w_gate_up E4M3 [E, 2I, H] (gate rows first), s_gate_up fp32
     [E, 2I/128, H/128]; w_down E4M3 [E, H, I], s_down fp32 [E, H/128, I/128] -> bf16 [T, H].
+    Both expert weights may instead be pack_experts outputs (bit-identical results).
     """
     device = require_device(x.device)
     if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
@@ -452,8 +485,14 @@ def moe_block_fp8(x, logits, w_gate_up, s_gate_up, w_down, s_down, *, top_k=2, n
         raise ValueError("expected fp32 router logits [T, E] with unit column stride")
     t, h = x.shape
     e = logits.shape[1]
+    packed = isinstance(w_gate_up, PackedExperts)
+    if packed != isinstance(w_down, PackedExperts):
+        raise ValueError("pack both expert weights (pack_experts) or neither")
     for wt in (w_gate_up, w_down):
-        if wt.dtype not in (torch.float8_e4m3fn, torch.uint8) or wt.ndim != 3 or not wt.is_contiguous():
+        if packed:
+            if wt.data.dtype != torch.uint8 or wt.data.numel() < wt.e * packed_weight_bytes(wt.n, wt.k):
+                raise ValueError("PackedExperts data is not a pack_experts output")
+        elif wt.dtype not in (torch.float8_e4m3fn, torch.uint8) or wt.ndim != 3 or not wt.is_contiguous():
             raise ValueError("expected contiguous E4M3 expert weights [E, N, K]")
     inter = w_gate_up.shape[1] // 2
     if w_gate_up.shape != (e, 2 * inter, h) or w_down.shape != (e, h, inter):
@@ -475,9 +514,11 @@ def moe_block_fp8(x, logits, w_gate_up, s_gate_up, w_down, s_down, *, top_k=2, n
         raise ValueError("out must be bf16 [T, H] with unit column stride on the same GPU")
     nat.check("gk_fp8_moe_bf16",
               nat.load().gk_fp8_moe_bf16(_ptr(x), t, h, x.stride(0), _ptr(logits), e, logits.stride(0), top_k,
-                                         _ptr(_u8(w_gate_up)), _ptr(s_gate_up), inter, _ptr(_u8(w_down)),
-                                         _ptr(s_down), _ptr(out), out.stride(0),
-                                         nat.GK_FLAG_NATIVE_HALF if native_half else 0, _ptr(ws), ws.numel(),
+                                         _ptr(w_gate_up.data if packed else _u8(w_gate_up)), _ptr(s_gate_up),
+                                         inter, _ptr(w_down.data if packed else _u8(w_down)), _ptr(s_down),
+                                         _ptr(out), out.stride(0),
+                                         (nat.GK_FLAG_NATIVE_HALF if native_half else 0)
+                                         | (nat.GK_FLAG_WEIGHT_PACKED if packed else 0), _ptr(ws), ws.numel(),
                                          _stream(device)))
     return out
 

@@ -284,7 +284,9 @@ gk_status gk_fp8_rms_norm_quant_bf16(const void* x, const void* residual, int64_
  * scales fp32 [E, 2I/128, H/128], w_dn E4M3 [E, H, I] with scales fp32
  * [E, H/128, I/128], y bf16 [T, H] (row stride ldy).  H and I multiples of
  * 128, E <= 256; x, y, weights 16-byte aligned with ldx, ldy multiples of 8.
- * flags: GK_FLAG_NATIVE_HALF only. */
+ * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_WEIGHT_PACKED: both w_gu and w_dn hold
+ * each expert's weights packed by gk_fp8_pack_weight, expert e at byte
+ * e * gk_fp8_packed_weight_bytes(n, k) (the results are bit-identical). */
 
 /* Padded row count of the expert-sorted layout: an upper bound of
  * sum_e round_up(count_e, 256), i.e. round_up(T*top_k + 255*E, 256). */

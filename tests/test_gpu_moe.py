@@ -87,6 +87,27 @@ def test_moe_small_full_parity(t, h, inter, e, k, native_half):
     assert max_rel <= block_fp8.MAX_REL_TOL and mean_rel <= block_fp8.MEAN_REL_TOL, (max_rel, mean_rel)
 
 
+@pytest.mark.parametrize("native_half", [False, True])
+def test_moe_packed_experts_bit_identical(native_half):
+    """Expert weights packed at load time (pack_experts) give the row-major layer's bits."""
+    t, h, inter, e, k = 300, 512, 384, 4, 2
+    gen = torch.Generator().manual_seed(41)
+    x = synth.activations(t, h, seed=42).cuda()
+    logits = torch.randn(t, e, generator=gen).cuda()
+    wg, sg, wd, sd = [], [], [], []
+    for i in range(e):
+        a, b = synth.weight(2 * inter, h, seed=50 + i, device="cuda")
+        c, d = synth.weight(h, inter, seed=60 + i, device="cuda")
+        wg.append(a); sg.append(b); wd.append(c); sd.append(d)
+    wg, sg, wd, sd = torch.stack(wg), torch.stack(sg), torch.stack(wd), torch.stack(sd)
+    y_row = ops.moe_block_fp8(x, logits, wg, sg, wd, sd, top_k=k, native_half=native_half)
+    y_pack = ops.moe_block_fp8(x, logits, ops.pack_experts(wg), sg, ops.pack_experts(wd), sd, top_k=k,
+                               native_half=native_half)
+    assert torch.equal(y_row.view(torch.int16), y_pack.view(torch.int16))
+    with pytest.raises(ValueError):
+        ops.moe_block_fp8(x, logits, ops.pack_experts(wg), sg, wd, sd, top_k=k)
+
+
 def test_moe_strided_output_and_reuse():
     x, logits, wg, sg, wd, sd = problem(96, 256, 256, 4, seed=77)
     xs = torch.zeros(96, 384, dtype=torch.bfloat16)
