@@ -60,7 +60,7 @@ typedef enum gk_status {
 #define GK_FLAG_FORCE_PREFILL 4u   /* force the LDS-tiled MFMA variant */
 #define GK_FLAG_FORCE_GENERIC 8u   /* force the any-shape variant */
 #define GK_FLAG_DECODE_LAYOUT 16u  /* act_quant / q GEMM only: quantized activations in the decode fragment layout */
-#define GK_FLAG_WEIGHT_PACKED 32u  /* block GEMMs: `w` holds weights packed by gk_fp8_pack_weight (not the generic variant) */
+#define GK_FLAG_WEIGHT_PACKED 32u  /* block GEMMs, MoE layer: weights packed by gk_fp8_pack_weight (not the generic variant) */
 
 /* Variants reported by gk_fp8_block_gemm_plan. */
 #define GK_VARIANT_DECODE 1
