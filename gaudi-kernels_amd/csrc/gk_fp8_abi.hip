@@ -34,6 +34,8 @@ constexpr const char* kOps[] = {
     "gk_fp8_channel_gemm_bf16_v1",  // MME + channel finish, fused (build-defined)
     "gk_silu_and_mul_bf16_v1",      // silu_and_mul_bf16.c, glue generic_dense_glue.cpp:196-236
     "gk_fp8_silu_mul_quant_bf16_v1",  // SiLU-and-mul fused with the 1x128 quantizer (build-defined)
+    "gk_gelu_and_mul_bf16_v1",      // gelu_and_mul_bf16.c, glue generic_dense_glue.cpp:424-458
+    "gk_fp8_gelu_mul_quant_bf16_v1",  // GELU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
     "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (build-defined)
     "gk_fp8_pack_weight_v1",        // load-time layout packing (fp8_codec.py:19 "a separate step")
@@ -515,6 +517,44 @@ gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t 
   if (st != GK_SUCCESS) return st;
   return from_hip(gk::launch_silu_mul_act_quant(static_cast<const uint16_t*>(gate_up), ld_in, static_cast<int>(rows),
                                                 static_cast<int>(width), static_cast<int>(m_pad),
+                                                static_cast<uint8_t*>(q), sa, (flags & GK_FLAG_NATIVE_HALF) != 0,
+                                                packed, static_cast<hipStream_t>(stream)));
+}
+
+// generic_dense_glue.cpp:424-431: approximate is 0 (exact GELU) or 1 (tanh form).
+gk_status gk_gelu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* out,
+                               int64_t ld_out, int approximate, void* stream) {
+  if (approximate != 0 && approximate != 1) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (!gate_up || !out) return GK_INVALID_ARGUMENT;
+  if (rows < 1 || width < 1 || rows > kMaxDim || width > kMaxDim / 2 || ld_in < 2 * width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ld_out < width) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(gate_up) | reinterpret_cast<uintptr_t>(out)) & 1) return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_gelu_and_mul(static_cast<const uint16_t*>(gate_up), ld_in, static_cast<int>(rows),
+                                          static_cast<int>(width), static_cast<uint16_t*>(out), ld_out,
+                                          approximate != 0, static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_gelu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in,
+                                     int approximate, void* q, float* sa, int64_t m_pad, uint32_t flags,
+                                     void* stream) {
+  if (approximate != 0 && approximate != 1) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (!gate_up || !q || !sa) return GK_INVALID_ARGUMENT;
+  if (rows < 1 || width < 1 || rows > kMaxDim || width > kMaxDim / 2 || ld_in < 2 * width)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (m_pad < rows || m_pad > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (flags & ~uint32_t{GK_FLAG_NATIVE_HALF | GK_FLAG_DECODE_LAYOUT}) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  const bool packed = (flags & GK_FLAG_DECODE_LAYOUT) != 0;
+  if (packed && m_pad != 16 && m_pad != 32 && m_pad != 64) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(gate_up) & 1) || (reinterpret_cast<uintptr_t>(q) & 7) ||
+      (reinterpret_cast<uintptr_t>(sa) & 3))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_gelu_mul_act_quant(static_cast<const uint16_t*>(gate_up), ld_in, static_cast<int>(rows),
+                                                static_cast<int>(width), approximate != 0, static_cast<int>(m_pad),
                                                 static_cast<uint8_t*>(q), sa, (flags & GK_FLAG_NATIVE_HALF) != 0,
                                                 packed, static_cast<hipStream_t>(stream)));
 }

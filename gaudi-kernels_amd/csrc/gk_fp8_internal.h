@@ -188,13 +188,18 @@ hipError_t launch_channel_finish(const float* partial, int64_t ldp, int rows, in
                                  const float* w_scales, const float* bias, uint16_t* y, int64_t ldy,
                                  hipStream_t stream);
 
-// ---- SiLU-and-mul (gk_fp8_act.hip) -------------------------------------------
+// ---- SiLU- and GELU-and-mul (gk_fp8_act.hip) ---------------------------------
 // in: bf16 [rows, 2*width] (gate | up), row stride ldi; out bf16 [rows, width].
 hipError_t launch_silu_and_mul(const uint16_t* in, int64_t ldi, int rows, int width, uint16_t* out, int64_t ldo,
                                hipStream_t stream);
 // Fused with the 1x128 quantizer: outputs as launch_act_quant (group-major or packed).
 hipError_t launch_silu_mul_act_quant(const uint16_t* in, int64_t ldi, int rows, int width, int Mpad, uint8_t* q,
                                      float* sa, bool half, bool packed, hipStream_t stream);
+// GELU-and-mul (approximate: the tanh form), plain and fused, same layouts.
+hipError_t launch_gelu_and_mul(const uint16_t* in, int64_t ldi, int rows, int width, uint16_t* out, int64_t ldo,
+                               bool approximate, hipStream_t stream);
+hipError_t launch_gelu_mul_act_quant(const uint16_t* in, int64_t ldi, int rows, int width, bool approximate,
+                                     int Mpad, uint8_t* q, float* sa, bool half, bool packed, hipStream_t stream);
 
 // ---- MoE (gk_fp8_moe.hip) ------------------------------------------------------
 // Workspace pieces of one MoE layer call (device pointers).

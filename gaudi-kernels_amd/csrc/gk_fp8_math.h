@@ -107,6 +107,32 @@ __host__ __device__ inline float silu_ref(float g) {
   return g / (1.0f + expf(-g));
 }
 
+// GELU of the reference's gk_gelu_and_mul_bf16_v1 (csrc/tpc/generic_dense/
+// gelu_and_mul_bf16.c:4-49): approximate = 0 is the exact GELU
+// x * erfc(-x / sqrt(2)) / 2, approximate = 1 the tanh form
+// x * sigmoid(2 sqrt(2/pi) (x + 0.044715 x^3)), both in fp32 from the
+// device library's erfcf / expf (the reference evaluates its own polynomials;
+// its test bounds both against fp64, tests/track_a_device_verify.cpp:274-286).
+// As there: +inf -> +inf, -inf -> 0, NaN -> NaN, and the tanh form is 0 for
+// x <= -15 (tpc_math_safe.h:149), where the fp64 value is below the fp32
+// range anyway.
+__host__ __device__ inline float gelu_erf_ref(float x) {
+  if (x != x) return x;
+  if (x == __builtin_huge_valf()) return x;
+  if (x == -__builtin_huge_valf()) return 0.0f;
+  return 0.5f * x * erfcf(-x * 0.70710678118654752f);
+}
+
+__host__ __device__ inline float gelu_tanh_ref(float x) {
+  if (x != x) return x;
+  if (x == __builtin_huge_valf()) return x;
+  if (x <= -15.0f) return 0.0f;
+  const float u = 1.5957691216057308f * (x + 0.044715f * x * x * x);
+  if (u >= 0.0f) return x / (1.0f + expf(-u));
+  const float e = expf(u);
+  return x * (e / (1.0f + e));
+}
+
 __host__ __device__ inline uint16_t bf16_rne(float v) {
   const uint32_t b = f32_bits(v);
   if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;

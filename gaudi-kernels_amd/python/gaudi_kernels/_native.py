@@ -82,6 +82,9 @@ SIGNATURES = {
                                           _c_i64, _c_u32, _c_vp]),
     "gk_silu_and_mul_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]),
     "gk_fp8_silu_mul_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _fp, _c_i64, _c_u32, _c_vp]),
+    "gk_gelu_and_mul_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),
+    "gk_fp8_gelu_mul_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _fp, _c_i64, _c_u32,
+                                            _c_vp]),
     "gk_rms_norm_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, ctypes.c_float, ctypes.c_float, _c_vp,
                                   _c_i64, _c_vp]),
     "gk_fused_add_rms_norm_bf16": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp, ctypes.c_float,

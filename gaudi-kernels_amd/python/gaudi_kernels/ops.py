@@ -371,6 +371,38 @@ def silu_mul_quant(gate_up, *, native_half=False, m_pad=None, decode_layout=Fals
     return q, sa
 
 
+def gelu_and_mul(gate_up, *, approximate=False, out=None):
+    """bf16 [rows, 2W] (gate | up) -> bf16 [rows, W] = bf16(gelu(gate) * up) (gk_gelu_and_mul_bf16_v1);
+    approximate=True is the tanh form."""
+    device = require_device(gate_up.device)
+    rows, width = _check_gate_up(gate_up, device)
+    if out is None:
+        out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    elif out.dtype != torch.bfloat16 or out.shape != (rows, width) or out.stride(1) != 1 or out.device != device:
+        raise ValueError("out must be bf16 [rows, W] with unit column stride on the same GPU")
+    nat.check("gk_gelu_and_mul_bf16",
+              nat.load().gk_gelu_and_mul_bf16(_ptr(gate_up), rows, width, gate_up.stride(0), _ptr(out),
+                                              out.stride(0), int(bool(approximate)), _stream(device)))
+    return out
+
+
+def gelu_mul_quant(gate_up, *, approximate=False, native_half=False, m_pad=None, decode_layout=False):
+    """GELU-and-mul fused with the 1x128 quantizer -> (codes [G, m_pad, 128], sa [G, m_pad]) as act_quant
+    of gelu_and_mul(gate_up) would give; decode_layout as in act_quant."""
+    device = require_device(gate_up.device)
+    rows, width = _check_gate_up(gate_up, device)
+    g = (width + 127) // 128
+    m_pad = (16 * decode_tiles(rows) if decode_layout else rows) if m_pad is None else m_pad
+    q = torch.empty((g, m_pad, 128), dtype=torch.uint8, device=device)
+    sa = torch.empty((g, m_pad), dtype=torch.float32, device=device)
+    flags = (nat.GK_FLAG_NATIVE_HALF if native_half else 0) | (nat.GK_FLAG_DECODE_LAYOUT if decode_layout else 0)
+    nat.check("gk_fp8_gelu_mul_quant_bf16",
+              nat.load().gk_fp8_gelu_mul_quant_bf16(_ptr(gate_up), rows, width, gate_up.stride(0),
+                                                    int(bool(approximate)), _ptr(q), _ptr(sa), m_pad, flags,
+                                                    _stream(device)))
+    return q, sa
+
+
 def _check_rows(t, name, device, width=None):
     if t.dtype != torch.bfloat16 or t.ndim != 2 or t.stride(1) != 1 or t.device != device:
         raise ValueError(f"{name} must be a 2-D bf16 tensor with unit column stride on the GPU")

@@ -234,6 +234,24 @@ gk_status gk_silu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width,
 gk_status gk_fp8_silu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* q,
                                      float* sa, int64_t m_pad, uint32_t flags, void* stream);
 
+/* The reference's gk_gelu_and_mul_bf16_v1 (csrc/tpc/generic_dense/
+ * gelu_and_mul_bf16.c:4-49, glue generic_dense_glue.cpp:424-458): shape rules
+ * of gk_silu_and_mul_bf16, out = bf16(gelu(gate) * up) with the product in
+ * fp32; approximate = 0 is the exact GELU x * erfc(-x/sqrt(2)) / 2, 1 the tanh
+ * form x * sigmoid(2 sqrt(2/pi) (x + 0.044715 x^3)) (0 for x <= -15); any
+ * other value -> GK_UNSUPPORTED_LAYER_CONFIGURATION.  fp32 evaluation through
+ * the device library's erfcf / expf; the output is within one bf16 ulp of
+ * the fp64 value (the reference test's bound). */
+gk_status gk_gelu_and_mul_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in, void* out,
+                               int64_t ld_out, int approximate, void* stream);
+
+/* The same products quantized per 1x128 group (no reference op), as
+ * gk_fp8_silu_mul_quant_bf16: codes and scales exactly as
+ * gk_fp8_act_quant_bf16 would write for the output of gk_gelu_and_mul_bf16. */
+gk_status gk_fp8_gelu_mul_quant_bf16(const void* gate_up, int64_t rows, int64_t width, int64_t ld_in,
+                                     int approximate, void* q, float* sa, int64_t m_pad, uint32_t flags,
+                                     void* stream);
+
 /* ---- RMSNorm ------------------------------------------------------------------ */
 
 /* The reference's gk_rms_norm_bf16_v1 (csrc/tpc/generic_dense/rms_norm_bf16.c:4-53,
