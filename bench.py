@@ -1,6 +1,6 @@
 """Benchmark of the MI355X block-FP8 W8A8 GEMM (BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|qkv|prefill|mlp|moe]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|qkv|side|prefill|mlp|moe]
 
 Workload (one "step"): BASELINE.json configs[1] decode sweep -- one block-FP8
 GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
@@ -210,7 +210,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["decode", "qkv", "prefill", "mlp", "moe"], default=None)
+    ap.add_argument("--only", choices=["decode", "qkv", "side", "prefill", "mlp", "moe"], default=None)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print per-kernel, per-grid tables of a rocprofv3 csv output directory and exit")
     args = ap.parse_args()
@@ -350,6 +350,67 @@ def main():
         result["qkv_chain"] = chain
         log(f"[bench] qkv chain (fused add + RMSNorm -> QKV GEMM): {chain}")
         del rot
+        torch.cuda.empty_cache()
+
+    # ---- the path's neighbours: load-time codec and packing, per-token / per-channel GEMM, gated
+    # activations fused with the quantizer (side measurements, bytes / FLOPs as stated per entry) ----------
+    if args.only in (None, "side"):
+        side = {}
+        w4, s4 = synth.weight(7168, 7168, seed=4000)
+        w4d, s4d = w4.cuda(), s4.cuda()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+        def timed_sync(fn, reps=10):
+            fn()
+            torch.cuda.synchronize()
+            ev0.record()
+            for _ in range(reps):
+                fn()
+            ev1.record()
+            torch.cuda.synchronize()
+            return ev0.elapsed_time(ev1) / reps
+
+        # codec: 2 B per code (read + write) + 8 B per scale; the call reads a status word back (synchronizes)
+        t = timed_sync(lambda: ops.codec_ocp_to_half(w4d, s4d))
+        side["codec_ocp_to_half_51M"] = {"us": round(t * 1e3, 1),
+                                         "GBps": round((2 * w4.numel() + 8 * s4.numel()) / (t * 1e-3) / 1e9, 1)}
+        t = time_loop(lambda: ops.pack_weight(w4d), 20, 3)  # 2 B per weight byte
+        side["pack_weight_51M"] = {"us": round(t * 1e3, 1), "GBps": round(2 * w4.numel() / (t * 1e-3) / 1e9, 1)}
+        # per-token / per-channel: token quantizer + channel GEMM, N = 6144, K = 4096 decode and config 4 prefill
+        sw2 = (torch.rand(n, generator=torch.Generator().manual_seed(7)) + 0.5).cuda()
+        wch = Rotation(synth.weight(n, k, seed=2000)[0], torch.zeros(1), min_bytes=MALL_ROTATE_BYTES)
+        for m in (1, 16):
+            xm = synth.activations(m, k, seed=2400 + m).cuda()
+
+            def chan():
+                q, sa = ops.token_quant(xm)
+                ops.channel_gemm(q, sa, wch.next()[0], sw2)
+
+            t = time_loop(chan, 100, 10)
+            side[f"token_channel_gemm_m{m}"] = {"us": round(t * 1e3, 2),
+                                                "GBps": round((n * k + 2 * m * k + 2 * m * n + 4 * n) / (t * 1e-3) / 1e9, 1)}
+        del wch
+        x4 = synth.activations(4096, 7168, seed=4001).cuda()
+        sw4 = (torch.rand(7168, generator=torch.Generator().manual_seed(8)) + 0.5).cuda()
+
+        def chan4():
+            q, sa = ops.token_quant(x4)
+            ops.channel_gemm(q, sa, w4d, sw4)
+
+        t = time_loop(chan4, 10, 2)
+        side["token_channel_gemm_m4096"] = {"us": round(t * 1e3, 1),
+                                            "TFLOPs": round(gemm_flops(4096, 7168, 7168) / (t * 1e-3) / 1e12, 1)}
+        # gated activation + 1x128 quantizer: 4 B in, 1 B + 4/128 B out per output element
+        for rows in (16, 4096):
+            gu = synth.activations(rows, 2 * 14336, seed=2500 + rows).cuda()
+            per = rows * 14336 * (4 + 1 + 4 / 128)
+            for name, fn in (("silu_mul_quant", lambda: ops.silu_mul_quant(gu)),
+                             ("gelu_mul_quant", lambda: ops.gelu_mul_quant(gu))):
+                t = time_loop(fn, 50, 5)
+                side[f"{name}_{rows}x14336"] = {"us": round(t * 1e3, 2), "GBps": round(per / (t * 1e-3) / 1e9, 1)}
+        result["side_ops"] = side
+        log(f"[bench] side ops: {side}")
+        del w4d, s4d, x4
         torch.cuda.empty_cache()
 
     # ---- config 3: MLP pair decode at M=16 ------------------------------------------------------
