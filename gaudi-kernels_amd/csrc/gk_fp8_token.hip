@@ -50,26 +50,52 @@ __device__ inline uint2 token_codes8(uint4 raw, float s, float r) {
   return make_uint2(codec_half4(out[0]), codec_half4(out[1]));
 }
 
+__device__ inline uint4 token_load8(const uint16_t* xr, int c, int vec_ok) {
+  if (vec_ok) return *reinterpret_cast<const uint4*>(xr + c);
+  uint32_t h[8];
+  for (int j = 0; j < 8; ++j) h[j] = xr[c + j];
+  return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+}
+
+__device__ inline float abs_max8(float m, uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bits_f32(w[i] << 16)), fabsf(bits_f32(w[i] & 0xffff0000u))));
+  return m;
+}
+
+// One workgroup per row.  Rows of up to kTokKeep * 2048 elements stay in
+// registers between the max and the quantization (one read of x); wider
+// rows are read again for the second pass.
+constexpr int kTokKeep = 4;
+
 __global__ __launch_bounds__(kTokThreads) void token_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                   int width, uint8_t* __restrict__ q, int64_t ldq,
                                                                   float* __restrict__ scales, int vec_ok) {
   __shared__ float wmax[kTokThreads / 64];
   const int row = blockIdx.x, tid = threadIdx.x;
   const uint16_t* xr = x + static_cast<int64_t>(row) * ldx;
+  constexpr int kStep = kTokThreads * 8;
+  const bool keep = width <= kTokKeep * kStep;
+  uint4 held[kTokKeep];
   float m = 0.0f;
-  for (int c = tid * 8; c < width; c += kTokThreads * 8) {
-    if (vec_ok) {
-      const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if (keep) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        m = fmaxf(m, fmaxf(fabsf(bits_f32(w[i] << 16)), fabsf(bits_f32(w[i] & 0xffff0000u))));
-    } else {
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(bf16_value(xr[c + j])));
+    for (int p = 0; p < kTokKeep; ++p) {
+      const int c = tid * 8 + p * kStep;
+      held[p] = make_uint4(0u, 0u, 0u, 0u);
+      if (c < width) {
+        held[p] = token_load8(xr, c, vec_ok);
+        m = abs_max8(m, held[p]);
+      }
     }
+  } else {
+    for (int c = tid * 8; c < width; c += kStep) m = abs_max8(m, token_load8(xr, c, vec_ok));
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  // |x| are non-negative: the maximum over 16 lanes in DPP steps, then across the 4 rows of 16 and the waves
+  m = __uint_as_float(row_max16_bits(m));
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
   if ((tid & 63) == 0) wmax[tid >> 6] = m;
   __syncthreads();
   m = wmax[0];
@@ -79,16 +105,15 @@ __global__ __launch_bounds__(kTokThreads) void token_quant_kernel(const uint16_t
   const float s = token_scale(m);
   const float r = 1.0f / s;
   uint8_t* qr = q + static_cast<int64_t>(row) * ldq;
-  for (int c = tid * 8; c < width; c += kTokThreads * 8) {
-    uint4 v;
-    if (vec_ok) {
-      v = *reinterpret_cast<const uint4*>(xr + c);
-    } else {
-      uint32_t h[8];
-      for (int j = 0; j < 8; ++j) h[j] = xr[c + j];
-      v = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+  if (keep) {
+#pragma unroll
+    for (int p = 0; p < kTokKeep; ++p) {
+      const int c = tid * 8 + p * kStep;
+      if (c < width) *reinterpret_cast<uint2*>(qr + c) = token_codes8(held[p], s, r);
     }
-    *reinterpret_cast<uint2*>(qr + c) = token_codes8(v, s, r);
+  } else {
+    for (int c = tid * 8; c < width; c += kStep)
+      *reinterpret_cast<uint2*>(qr + c) = token_codes8(token_load8(xr, c, vec_ok), s, r);
   }
   if (tid == 0) scales[row] = 2.0f * s;
 }
