@@ -9,8 +9,12 @@
 // Structure (one workgroup = 8 waves, 4 along N x 2 along M, 64 x 128 each):
 //   * Stage = one 128-K group: the 256 x 128-byte weight tile and the 256 x
 //     128-byte activation tile, copied global -> LDS with direct-to-LDS loads
-//     (global_load_lds_dwordx4: each wave instruction moves 8 rows x 128 B).
-//     Two stages ping-pong; stage g+1 is loaded while stage g is computed.
+//     (buffer_load_dwordx4 ... lds: each wave instruction moves 8 rows x 128 B).
+//     Weights rotate through three LDS stages and are loaded two steps ahead
+//     (they come from HBM); activations rotate through two and are loaded one
+//     step ahead (they are re-read by every weight panel and come from L2).
+//     Step g waits only for its own tiles: the weights of step g+1 and the
+//     token scales stay in flight across its barrier.
 //   * LDS rows are 128 bytes with the 16-byte chunk c of row r stored at slot
 //     c ^ ((r >> 1) & 7): sixteen consecutive rows reading one chunk hit 16
 //     distinct 16-byte bank groups (measured: zero LDS bank conflicts).
@@ -32,8 +36,17 @@ namespace {
 
 constexpr int kBN = 256, kBM = 256;        // workgroup tile (weight rows x tokens)
 constexpr int kTile = 256 * 128;           // one operand tile of one group in LDS
-constexpr int kStageBytes = 2 * kTile;     // weights + activations
-constexpr int kLdsBytes = 2 * kStageBytes; // two stages: 128 KB of the 160 KB LDS
+constexpr int kWStages = 3, kAStages = 2;  // weight / activation stages
+constexpr int kLdsBytes = (kWStages + kAStages) * kTile;  // 160 KB: all of the LDS
+
+// Word 3 of a raw buffer resource on gfx9-family parts (data format 32; the
+// format is not used by the dword loads here, but must be valid).
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ inline __attribute__((address_space(3))) void* lds_ptr(uint8_t* p) {
+  return reinterpret_cast<__attribute__((address_space(3))) void*>(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
 
 __device__ inline u32x4 lds_read16(uint32_t addr) {
   u32x4 r;
@@ -119,7 +132,6 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   // 32-row blocks of this wave's 128 rows that hold live rows (wave-uniform)
   const int jlive = min(4, max(0, (live - wm * 128 + 31) / 32));
   const int gbeg = (G * part) / kparts, gend = (G * (part + 1)) / kparts;
-  const int64_t qstep = static_cast<int64_t>(Mpad) * 128;
 
   // Loader: wave w fills weight rows and activation rows [32 w, 32 w + 32) of
   // the stage, 4 + 4 instructions of 8 rows; lane -> (row r0 + 8 i, slot ls)
@@ -129,38 +141,67 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   int lcs[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ (((r0 + 8 * i) >> 1) & 7)) * 16;
-  // Per-lane 32-bit offsets from wave-uniform bases (the loads then use the
-  // scalar-base + 32-bit-offset form: fewer VGPRs than 64-bit pointers).
+  // Loader addresses: a wave-uniform base (scalar registers) plus a per-lane
+  // 32-bit offset.  Packed weights need one lane offset (lane * 16) and the
+  // group-major activations two (the chunk key of rows r0 + 8 i alternates with
+  // i % 2); row-major weights and per-token activations clamp every row, so
+  // they keep one offset per instruction.
   const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;  // packed: tile n0/16 starts at (n0/16) * G * 2048 = n0 * K
   const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * (CH ? ldq : 128);
   const int nmax = N - 1 - n0, mmax = M - 1 - m0;
-  const uint32_t gstep = CH ? 128u : static_cast<uint32_t>(qstep);  // activation bytes from group to group
+  const int nblk = ((N + 15) >> 4) - 1 - (n0 >> 4);  // last 16-row block of the panel
+  const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;
+  const uint32_t bl0 = lr * 128 + ((ls ^ (lr >> 1)) << 4), bl1 = lr * 128 + ((ls ^ (lr >> 1) ^ 4) << 4);
   uint32_t aoff[4], boff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    // packed: block 2 wave + i/2 of the tile (blocks past the last re-read the last one), half i % 2
-    const int blk = min(2 * wave + (i >> 1), ((N + 15) >> 4) - 1 - (n0 >> 4));
-    aoff[i] = WPACK ? static_cast<uint32_t>(blk) * static_cast<uint32_t>(G) * 2048u +
-                          static_cast<uint32_t>((i & 1) * 1024 + lane * 16)
-                    : static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
-    boff[i] = CH ? static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i])
-                 : static_cast<uint32_t>((r0 + 8 * i) * 128 + lcs[i]);
+    aoff[i] = static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
+    boff[i] = static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i]);
   }
-  constexpr uint32_t kAG = WPACK ? 2048u : 128u;  // weight bytes from group to group
   // Activation rows [32 wave, +32) past the tile's live rows are never read
   // (every wave skips its 32-row blocks past them): their copies are skipped.
   const bool act_live = wave * 32 < live;  // wave-uniform
-  auto issue = [&](int g, int stage) {
-    uint8_t* base = smem + stage * kStageBytes + wave * 32 * 128;
+  // Tile copies are buffer loads with the LDS bit (buffer_load_dwordx4 ... lds):
+  // the compiler counts them exactly, so the token-scale loads issued between
+  // them get partial vmcnt waits.  (With the FLAT-encoded global_load_lds it
+  // waits for every load in flight before the first use of any loaded value.)
+  // Offsets stay below 2^32 (prefill256_fits, launch_gemm_channel256); the
+  // records field is at its maximum, so no load is range-clipped.
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(asrc), 0, -1, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t arsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bsrc), 0, -1, kBufferWord3);
+  // Exactly four load instructions each: the step's wait counts on it.
+  auto issue_w = [&](int g, int ws) {
+    uint8_t* base = smem + ws * kTile + wave * 32 * 128;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(asrc + static_cast<uint64_t>(aoff[i] + static_cast<uint32_t>(g) * kAG),
-                                       base + i * 1024, 16, 0, 0);
-    if (act_live) {
+    for (int i = 0; i < 4; ++i) {
+      uint32_t vo, so;
+      if (WPACK) {  // block 2 wave + i/2 of the tile (blocks past the last re-read the last one), half i % 2
+        const int blk = min(2 * wave + (i >> 1), nblk);
+        vo = lane16;
+        so = static_cast<uint32_t>((blk * G + g) * 2048 + (i & 1) * 1024);
+      } else {
+        vo = aoff[i];
+        so = static_cast<uint32_t>(g) * 128u;
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, lds_ptr(base + i * 1024), 16, vo, so, 0, 0);
+    }
+  };
+  auto issue_a = [&](int g, int as) {
+    if (!act_live) return;
+    uint8_t* base = smem + (kWStages + as) * kTile + wave * 32 * 128;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_global_load_lds(bsrc + static_cast<uint64_t>(boff[i] + static_cast<uint32_t>(g) * gstep),
-                                         base + kTile + i * 1024, 16, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      uint32_t vo, so;
+      if (CH) {
+        vo = boff[i];
+        so = static_cast<uint32_t>(g) * 128u;
+      } else {  // rows r0 + 8 i of group g: (wave * 32 + 8 i) * 128 + the lane's row and chunk
+        vo = (i & 1) ? bl1 : bl0;
+        so = static_cast<uint32_t>(g) * static_cast<uint32_t>(Mpad * 128) + static_cast<uint32_t>((wave * 32 + 8 * i) * 128);
+      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, lds_ptr(base + i * 1024), 16, vo, so, 0, 0);
     }
   };
 
@@ -174,7 +215,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const uint32_t ya00 = WPACK ? 0u : xo00, ya01 = WPACK ? 1024u : xo01;
   const uint32_t ya10 = WPACK ? 512u : xo10, ya11 = WPACK ? 1536u : xo11;
   const uint32_t lbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
-  const uint32_t arow = WPACK ? pa : (wn * 64 + fr) * 128, brow = kTile + (wm * 128 + fr) * 128;
+  const uint32_t arow = WPACK ? pa : (wn * 64 + fr) * 128, brow = kWStages * kTile + (wm * 128 + fr) * 128;
   const float* sap = sa + (m0 + wm * 128 + fr);  // + 32 j + g * Mpad  (m0 + 256 <= Mpad)
   const float* swp = sw + static_cast<int64_t>(min(n0 + wn * 64, N - 1) >> 7) * G;
 
@@ -186,57 +227,90 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  issue(gbeg, 0);
-  for (int g = gbeg; g < gend; ++g) {
-    const int stage = (g - gbeg) & 1;
-    float sav[4] = {0.0f, 0.0f, 0.0f, 0.0f}, swg = 0.0f;
+  // Issue order in step g: token scales of g + 1 (before the wait), then, past
+  // the barrier, activations of g + 1 and weights of g + 2.  Weights are issued
+  // at every step (past the last group they re-read it into a stage no later
+  // step reads), so at the top of step g the loads younger than step g's
+  // activations are exactly weights g + 1 and scales g + 1: vmcnt(8) (vmcnt(4)
+  // in the CH form, which loads no token scales) completes step g's tiles and
+  // leaves those in flight.  The compiler tracks the scale loads itself; it
+  // counts the buffer loads exactly, so its waits for them are partial too.
+  float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // token scales of the next step
+  auto load_sav = [&](int g) {
     if (!CH) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sav[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
+      for (int j = 0; j < 4; ++j) sv[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
+    }
+  };
+  // (An empty K range, a K-split half with no groups, stores zeros.)
+  if (gbeg < gend) {
+    issue_w(gbeg, 0);
+    load_sav(gbeg);
+    issue_a(gbeg, 0);
+    issue_w(min(gbeg + 1, gend - 1), 1);
+    int ws = 0, as = 0;  // stages of step g
+    int g = gbeg;
+    do {
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-      swg = HALF ? 2.0f * swp[g] : swp[g];
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of stage g (and everything older) are done
-    __syncthreads();                // ... for every wave; all reads of stage g-1 are done too
-    if (g + 1 < gend) issue(g + 1, stage ^ 1);
-    if (jlive == 0) continue;  // no live rows for this wave (it still takes part in the loads and barriers)
-    const uint32_t A = lbase + stage * kStageBytes + arow;
-    const uint32_t B = lbase + stage * kStageBytes + brow;
-    v8i a00 = lds_frag(A + ya00, A + ya01), a01 = lds_frag(A + ya10, A + ya11);
-    v8i a10 = lds_frag(A + 4096 + ya00, A + 4096 + ya01), a11 = lds_frag(A + 4096 + ya10, A + 4096 + ya11);
-    v8i b0 = lds_frag(B + xo00, B + xo01), b1 = lds_frag(B + xo10, B + xo11);
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a00), "+v"(a01), "+v"(a10), "+v"(a11), "+v"(b0), "+v"(b1));
-    if (HALF) {
-      a00 = half_codes(a00); a01 = half_codes(a01); a10 = half_codes(a10); a11 = half_codes(a11);
-    }
+      const float swg = CH ? 0.0f : (HALF ? 2.0f * swp[g] : swp[g]);
+      float fj[4];  // promotion factors of step g
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < jlive) {  // wave-uniform; j is a constant after unrolling, so acc stays in registers
-        if (j > 0) {
-          b0 = lds_frag(B + j * 4096 + xo00, B + j * 4096 + xo01);
-          b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
-        }
-        if (CH) {
-          acc[0][j] = mfma32_f8(a00, b0, acc[0][j]);
-          acc[1][j] = mfma32_f8(a10, b0, acc[1][j]);
-          acc[0][j] = mfma32_f8(a01, b1, acc[0][j]);
-          acc[1][j] = mfma32_f8(a11, b1, acc[1][j]);
-        } else {
-          const float f = sav[j] * swg;
-          v16f t0, t1;
+      for (int j = 0; j < 4; ++j) fj[j] = sv[j] * swg;
+      load_sav(min(g + 1, gend - 1));
+      // This wave's tile loads of step g are done: vmcnt(8) or vmcnt(4), expcnt(7), lgkmcnt(15).
+      if (CH)
+        __builtin_amdgcn_s_waitcnt(0x0F74);
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F78);
+      // ... for every wave; all fragment reads of step g-1 are done too (each
+      // step's reads end with lgkmcnt(0)).  A bare barrier: __syncthreads()'s
+      // release fence would wait for the weight loads still in flight.
+      __builtin_amdgcn_s_barrier();
+      if (g + 1 < gend) issue_a(g + 1, as ^ 1);
+      issue_w(min(g + 2, gend - 1), ws == 0 ? 2 : ws - 1);  // the stage step g-1 used
+      const uint32_t A = lbase + ws * kTile + arow;
+      const uint32_t B = lbase + as * kTile + brow;
+      ws = ws == 2 ? 0 : ws + 1;
+      as ^= 1;
+      if (jlive == 0) continue;  // no live rows for this wave (it still takes part in the loads and barriers)
+      v8i a00 = lds_frag(A + ya00, A + ya01), a01 = lds_frag(A + ya10, A + ya11);
+      v8i a10 = lds_frag(A + 4096 + ya00, A + 4096 + ya01), a11 = lds_frag(A + 4096 + ya10, A + 4096 + ya11);
+      v8i b0 = lds_frag(B + xo00, B + xo01), b1 = lds_frag(B + xo10, B + xo11);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a00), "+v"(a01), "+v"(a10), "+v"(a11), "+v"(b0), "+v"(b1));
+      if (HALF) {
+        a00 = half_codes(a00); a01 = half_codes(a01); a10 = half_codes(a10); a11 = half_codes(a11);
+      }
 #pragma unroll
-          for (int r = 0; r < 16; ++r) { t0[r] = 0.0f; t1[r] = 0.0f; }
-          t0 = mfma32_f8(a00, b0, t0);
-          t1 = mfma32_f8(a10, b0, t1);
-          t0 = mfma32_f8(a01, b1, t0);
-          t1 = mfma32_f8(a11, b1, t1);
-          promote(acc[0][j], t0, f);
-          promote(acc[1][j], t1, f);
+      for (int j = 0; j < 4; ++j) {
+        if (j < jlive) {  // wave-uniform; j is a constant after unrolling, so acc stays in registers
+          if (j > 0) {
+            b0 = lds_frag(B + j * 4096 + xo00, B + j * 4096 + xo01);
+            b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
+          }
+          if (CH) {
+            acc[0][j] = mfma32_f8(a00, b0, acc[0][j]);
+            acc[1][j] = mfma32_f8(a10, b0, acc[1][j]);
+            acc[0][j] = mfma32_f8(a01, b1, acc[0][j]);
+            acc[1][j] = mfma32_f8(a11, b1, acc[1][j]);
+          } else {
+            const float f = fj[j];
+            v16f t;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) t[r] = 0.0f;
+            t = mfma32_f8(a01, b1, mfma32_f8(a00, b0, t));
+            promote(acc[0][j], t, f);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) t[r] = 0.0f;
+            t = mfma32_f8(a11, b1, mfma32_f8(a10, b0, t));
+            promote(acc[1][j], t, f);
+          }
         }
       }
-    }
+    } while (++g < gend);
   }
+
+  __builtin_amdgcn_s_waitcnt(0);  // the re-read weight loads still in flight write LDS
 
   if (CH) {
 #pragma unroll
