@@ -26,10 +26,14 @@ namespace {
 // ---- routing: one workgroup of 1024 threads ---------------------------------------
 // Phase 1: per token, the top-k experts (strictly greater wins; ties keep the
 // lower index) and softmax weights; an LDS histogram of expert counts.
-// Phase 2: padded segment starts.  Phase 3: for each expert, a block-wide
-// exclusive prefix count over tokens (in token order, 1024 at a time) gives
-// each slot's rank inside its expert -- stable, deterministic.
+// Phase 2: padded segment starts.  Phase 3, per chunk of 1024 tokens: each
+// wave ballots every expert over its 64 tokens (a token's rank among the
+// wave's tokens of that expert), the per-wave counts are prefix-summed over
+// the waves per expert, and a slot's row is its expert's start + the tokens of
+// that expert in earlier chunks and waves + its rank in the wave: rows are in
+// token order inside each expert -- stable, deterministic.
 constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
 
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* __restrict__ logits, int T, int E,
                                                                   int64_t ld, int top_k, int rows_max,
@@ -37,7 +41,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
   __shared__ int counts[kMoeMaxExperts];
   __shared__ int offs[kMoeMaxExperts + 1];
   __shared__ int carry[kMoeMaxExperts];
-  __shared__ int wave_sum[kRouteThreads / 64];
+  __shared__ int wcnt[kRouteWaves][kMoeMaxExperts];  // per chunk: wave counts, then their exclusive prefix
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int e = tid; e < E; e += kRouteThreads) counts[e] = 0;
   for (int i = tid; i < rows_max; i += kRouteThreads) r.row_token[i] = -1;
@@ -92,27 +96,36 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
     const bool live = t < T;
     const int e0 = live ? r.ids[t * top_k] : -1;
     const int e1 = (live && top_k == 2) ? r.ids[t * 2 + 1] : -1;
-    for (int e = 0; e < E; ++e) {
-      const int slot = (e0 == e) ? 0 : (e1 == e) ? 1 : -1;  // a token picks an expert at most once
-      const unsigned long long mask = __ballot(slot >= 0);
-      const int below = __popcll(mask & ((1ull << lane) - 1ull));
-      if (lane == 0) wave_sum[wave] = __popcll(mask);
-      __syncthreads();
-      int before = 0;
-      for (int v = 0; v < wave; ++v) before += wave_sum[v];
-      if (slot >= 0) {
-        const int row = offs[e] + carry[e] + before + below;
-        r.row_token[row] = t;
-        r.row_of[t * top_k + slot] = row;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        int total = 0;
-        for (int v = 0; v < kRouteThreads / 64; ++v) total += wave_sum[v];
-        carry[e] += total;
-      }
-      __syncthreads();
+    const unsigned long long below_lane = (1ull << lane) - 1ull;
+    int rank0 = 0, rank1 = 0;
+    for (int e = 0; e < E; ++e) {  // a token picks an expert at most once
+      const unsigned long long mask = __ballot(e0 == e || e1 == e);
+      if (lane == 0) wcnt[wave][e] = __popcll(mask);
+      if (e0 == e) rank0 = __popcll(mask & below_lane);
+      if (e1 == e) rank1 = __popcll(mask & below_lane);
     }
+    __syncthreads();
+    for (int e = tid; e < E; e += kRouteThreads) {  // exclusive prefix over the waves, from the carry
+      int acc = carry[e];
+      for (int v = 0; v < kRouteWaves; ++v) {
+        const int c = wcnt[v][e];
+        wcnt[v][e] = acc;
+        acc += c;
+      }
+      carry[e] = acc;
+    }
+    __syncthreads();
+    if (e0 >= 0) {
+      const int row = offs[e0] + wcnt[wave][e0] + rank0;
+      r.row_token[row] = t;
+      r.row_of[t * top_k] = row;
+    }
+    if (e1 >= 0) {
+      const int row = offs[e1] + wcnt[wave][e1] + rank1;
+      r.row_token[row] = t;
+      r.row_of[t * 2 + 1] = row;
+    }
+    __syncthreads();  // the next chunk rewrites wcnt
   }
 }
 
