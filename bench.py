@@ -376,19 +376,22 @@ def main():
                                          "GBps": round((2 * w4.numel() + 8 * s4.numel()) / (t * 1e-3) / 1e9, 1)}
         t = time_loop(lambda: ops.pack_weight(w4d), 20, 3)  # 2 B per weight byte
         side["pack_weight_51M"] = {"us": round(t * 1e3, 1), "GBps": round(2 * w4.numel() / (t * 1e-3) / 1e9, 1)}
-        # per-token / per-channel: token quantizer + channel GEMM, N = 6144, K = 4096 decode and config 4 prefill
+        # per-token / per-channel: token quantizer + channel GEMM, N = 6144, K = 4096 decode (one fused launch,
+        # ops.token_channel_gemm; the two launches beside it) and config 4 prefill
         sw2 = (torch.rand(n, generator=torch.Generator().manual_seed(7)) + 0.5).cuda()
         wch = Rotation(synth.weight(n, k, seed=2000)[0], torch.zeros(1), min_bytes=MALL_ROTATE_BYTES)
         for m in (1, 16):
             xm = synth.activations(m, k, seed=2400 + m).cuda()
 
-            def chan():
+            def chan2():
                 q, sa = ops.token_quant(xm)
                 ops.channel_gemm(q, sa, wch.next()[0], sw2)
 
-            t = time_loop(chan, 100, 10)
+            t2 = time_loop(chan2, 100, 10)
+            t = time_loop(lambda: ops.token_channel_gemm(xm, wch.next()[0], sw2), 100, 10)
             side[f"token_channel_gemm_m{m}"] = {"us": round(t * 1e3, 2),
-                                                "GBps": round((n * k + 2 * m * k + 2 * m * n + 4 * n) / (t * 1e-3) / 1e9, 1)}
+                                                "GBps": round((n * k + 2 * m * k + 2 * m * n + 4 * n) / (t * 1e-3) / 1e9, 1),
+                                                "two_launch_us": round(t2 * 1e3, 2)}
         del wch
         x4 = synth.activations(4096, 7168, seed=4001).cuda()
         sw4 = (torch.rand(7168, generator=torch.Generator().manual_seed(8)) + 0.5).cuda()

@@ -32,6 +32,7 @@ constexpr const char* kOps[] = {
     "gk_fp8_token_quant_bf16_v1",   // activation_token.c:4-26, glue generic_fp8_glue.hpp:31-50
     "gk_fp8_channel_finish_bf16_v1",  // channel_finish.c:2-18, glue generic_fp8_glue.hpp:52-82
     "gk_fp8_channel_gemm_bf16_v1",  // MME + channel finish, fused (build-defined)
+    "gk_fp8_token_channel_gemm_bf16_v1",  // token quant + MME + channel finish, fused, M <= 16 (build-defined)
     "gk_silu_and_mul_bf16_v1",      // silu_and_mul_bf16.c, glue generic_dense_glue.cpp:196-236
     "gk_fp8_silu_mul_quant_bf16_v1",  // SiLU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_gelu_and_mul_bf16_v1",      // gelu_and_mul_bf16.c, glue generic_dense_glue.cpp:424-458
@@ -483,6 +484,29 @@ gk_status gk_fp8_channel_gemm_bf16(const void* q, int64_t ldq, const float* sa, 
   a.K = static_cast<int>(k); a.G = static_cast<int>(k / 128); a.Mpad = static_cast<int>(m); a.half_w = false;
   a.channel = true; a.ldq = ldq;
   return from_hip(gk::launch_gemm_channel(a, static_cast<hipStream_t>(stream)));
+}
+
+gk_status gk_fp8_token_channel_gemm_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, const void* w, int64_t n,
+                                         const float* sw, const float* bias, void* y, int64_t ldy, uint32_t flags,
+                                         void* stream) {
+  if (!x || !w || !sw || !y) return GK_INVALID_ARGUMENT;
+  if (flags) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  // the token quantizer's width rule (generic_fp8_glue.hpp:39-44) and the fused form's M <= 16
+  if (m < 1 || m > 16 || n < 1 || k < 128 || k % 128 || n > kMaxDim || k > kMaxDim || ldx < k)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldy < n) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || ldx % 8 || (reinterpret_cast<uintptr_t>(w) & 15) ||
+      ((reinterpret_cast<uintptr_t>(sw) | reinterpret_cast<uintptr_t>(bias)) & 3) ||
+      (reinterpret_cast<uintptr_t>(y) & 1))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  gk::GemmArgs a{};
+  a.qa = static_cast<const uint8_t*>(x); a.sa = nullptr; a.w = static_cast<const uint8_t*>(w); a.sw = sw;
+  a.bias = bias; a.y = static_cast<uint16_t*>(y); a.ldy = ldy; a.M = static_cast<int>(m);
+  a.N = static_cast<int>(n); a.K = static_cast<int>(k); a.G = static_cast<int>(k / 128);
+  a.Mpad = static_cast<int>(m); a.half_w = false; a.channel = true; a.ldq = ldx;
+  return from_hip(gk::launch_gemm_token_channel(a, static_cast<hipStream_t>(stream)));
 }
 
 // ---- SiLU-and-mul ----------------------------------------------------------------------

@@ -76,6 +76,15 @@ namespace gk {
 // scale per token sa[m] and per output channel sw[n]; the MFMAs accumulate
 // over all of K (no per-group promotion) and the epilogue applies
 // bf16(fma(p * sa[m], sw[n], bias[n])) (channel_finish.c:9-15).
+//
+// CH and XQ: the per-token quantizer fused in (sa unused).  A token's scale
+// needs the maximum |x| over its whole row, so each wave first takes the
+// maximum over its own groups (the XQ loader's lanes), the waves combine them
+// in LDS, and every lane forms s and 1/s of its four loader tokens and 2 s of
+// its output token; the main loop then encodes with the token quantizer's
+// token_codes8.  The maximum does not depend on the order (fmaxf drops NaN,
+// |x| >= +0), so codes, scales and results equal token quant + this kernel's
+// CH form bit for bit.
 template <int NW, int R, int U, bool HALF, bool QPACK, bool CH = false, bool WPACK = false, bool XQ = false,
           int MT = 1>
 __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __restrict__ qa,
@@ -90,6 +99,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   __shared__ __attribute__((aligned(16))) uint8_t tile[WPACK ? 1 : NW][2048];
   __shared__ __attribute__((aligned(16))) uint8_t xqbuf[XQ ? NW : 1][XQ ? U : 1][2048 + 64];  // codes + 16 scales
   __shared__ v4f red[NW][R][MT][64];
+  __shared__ float tmax[CH && XQ ? NW : 1][16];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int col = lane & 15, quad = lane >> 4;
@@ -148,6 +158,35 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
   uint8_t* buf = tile[WPACK ? 0 : wave];
 
+  // Fused per-token quantizer: s, 1/s of loader token 4 j + lane/16, 2 s of token col.
+  float tsc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, trc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, tcol2 = 0.0f;
+  if (CH && XQ) {
+    float mj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = gbeg; g < gend; ++g) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < xjn) mj[j] = abs_max8(mj[j], *reinterpret_cast<const uint4*>(xrow[j] + static_cast<int64_t>(g) * 256));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float m16 = __uint_as_float(row_max16_bits(mj[j]));  // over the 16 lanes of the token
+      if ((lane & 15) == 0) tmax[wave][4 * j + (lane >> 4)] = m16;
+    }
+    __syncthreads();
+    auto token_max = [&](int t) {
+      float m = tmax[0][t];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) m = fmaxf(m, tmax[v][t]);
+      return m == 0.0f ? 1.0f : m;  // an all-zero token (activation_token.c:16)
+    };
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      tsc[j] = token_scale(token_max(4 * j + (lane >> 4)));
+      trc[j] = 1.0f / tsc[j];
+    }
+    tcol2 = 2.0f * token_scale(token_max(col));
+  }
+
   v4f acc[R][MT];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -202,17 +241,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
         if (j >= xjn) continue;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          float sc;
-          const uint2 c = quant_group8(xb[u][j], true, HALF, &sc);
-          *reinterpret_cast<uint2*>(xq + u * (2048 + 64) + xwoff[j]) = c;
-          *reinterpret_cast<float*>(xq + u * (2048 + 64) + 2048 + 4 * (4 * j + (lane >> 4))) = sc;
+          if (CH) {
+            *reinterpret_cast<uint2*>(xq + u * (2048 + 64) + xwoff[j]) = token_codes8(xb[u][j], tsc[j], trc[j]);
+          } else {
+            float sc;
+            const uint2 c = quant_group8(xb[u][j], true, HALF, &sc);
+            *reinterpret_cast<uint2*>(xq + u * (2048 + 64) + xwoff[j]) = c;
+            *reinterpret_cast<float*>(xq + u * (2048 + 64) + 2048 + 4 * (4 * j + (lane >> 4))) = sc;
+          }
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {  // same wave: its LDS accesses complete in order
         const uint8_t* b = xq + u * (2048 + 64);
         bq[u] = pack8(*reinterpret_cast<const uint4*>(b + 16 * lane), *reinterpret_cast<const uint4*>(b + 1024 + 16 * lane));
-        sv[u][0] = *reinterpret_cast<const float*>(b + 2048 + 4 * col);
+        if (!CH) sv[u][0] = *reinterpret_cast<const float*>(b + 2048 + 4 * col);
       }
     }
 #pragma unroll
@@ -261,7 +304,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
     const int m = 16 * t + col, n = n0 + 16 * r + 4 * quad;
     if (CH) {
       if (m >= M) continue;
-      const float sam = sa[m];
+      const float sam = XQ ? tcol2 : sa[m];
       uint16_t* row = y + static_cast<int64_t>(m) * ldy + n;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -381,11 +424,22 @@ static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Per-token quantizer fused in: a.qa = bf16 x, a.ldq its row stride (elements).
+template <int NW, int R, int U, int MT>
+static hipError_t decode_token_channel_launch(const GemmArgs& a, hipStream_t stream) {
+  static_assert(MT == 1, "the fused per-token decode takes one token tile");
+  const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
+  gemm_decode_kernel<NW, R, U, false, false, true, false, true><<<grid, NW * 64, 0, stream>>>(
+      a.qa, nullptr, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq);
+  return hipGetLastError();
+}
+
 // Instantiated decode shapes (NW, R, U, MT); plan_decode_shape and
 // fused_quant_shape return only these (the per-channel decode: the first list).
 #define GK_DECODE_SHAPES1(X) X(2, 2, 4, 1) X(8, 2, 2, 1) X(8, 2, 4, 1) X(8, 1, 2, 1) X(16, 1, 2, 1)
-#define GK_DECODE_SHAPES(X) GK_DECODE_SHAPES1(X)                                               \
-  X(2, 2, 2, 1) X(2, 2, 1, 1) X(8, 2, 1, 1) X(8, 1, 1, 1) X(16, 1, 1, 1)                       \
+#define GK_DECODE_SHAPES_T1(X) GK_DECODE_SHAPES1(X) \
+  X(2, 2, 2, 1) X(2, 2, 1, 1) X(8, 2, 1, 1) X(8, 1, 1, 1) X(16, 1, 1, 1)
+#define GK_DECODE_SHAPES(X) GK_DECODE_SHAPES_T1(X)                                             \
   X(2, 2, 2, 2) X(8, 2, 1, 2) X(8, 2, 2, 2) X(8, 1, 1, 2) X(16, 1, 1, 2)                       \
   X(2, 2, 1, 4) X(8, 2, 1, 4) X(8, 1, 1, 4) X(16, 1, 1, 4)
 constexpr int decode_key(int nw, int r, int u, int mt) { return ((nw * 10 + r) * 10 + u) * 10 + mt; }
@@ -416,6 +470,20 @@ hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream) {
 #define GK_CASE(NW, R, U, MT) \
   case decode_key(NW, R, U, MT): return decode_channel_launch<NW, R, U, MT>(a, stream);
     GK_DECODE_SHAPES1(GK_CASE)
+#undef GK_CASE
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Fused per-token quantizer + per-channel decode, M <= 16: the shape of the
+// block path's fused quantizer (fused_quant_shape on row-major weights).
+hipError_t launch_gemm_token_channel(const GemmArgs& a, hipStream_t stream) {
+  if (a.M < 1 || a.M > 16) return hipErrorInvalidValue;
+  const DecodeShape d = fused_quant_shape(fit_group_step(plan_decode_shape(a.N, a.G, false, 1), a.G), a.G);
+  switch (decode_key(d.nw, d.r, d.u, d.mt)) {
+#define GK_CASE(NW, R, U, MT) \
+  case decode_key(NW, R, U, MT): return decode_token_channel_launch<NW, R, U, MT>(a, stream);
+    GK_DECODE_SHAPES_T1(GK_CASE)
 #undef GK_CASE
     default: return hipErrorInvalidValue;
   }

@@ -98,6 +98,42 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
 // Fragment-packed weights: for 16-row tile t and group g a 2 KB block at
 // (t * G + g) * 2048; piece (h, l) at h*1024 + 16 l = bytes [128 g + 32 (l/16)
 // + 16 h, +16) of row 16 t + l%16, zeros past N.  K % 128 == 0.
+// Per-token quantizer arithmetic (activation_token.c:4-26, activation_quant_common.h:3-30),
+// shared by the token quantizer and the decode kernel's fused per-token form.
+__device__ inline float token_scale(float m) {  // activation_quant_common.h:3-7
+  const float inv448 = 1.0f / 448.0f;
+  const float s0 = mul_rn(m, inv448);
+  const float res = fmaf(-s0, 448.0f, m);
+  return fmaf(res, inv448, s0);
+}
+
+// 8 bf16 values -> 8 half-range codes (as two packed dwords).
+__device__ inline uint2 token_codes8(uint4 raw, float s, float r) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t out[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float z[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float x = bits_f32(h ? (w[i] & 0xffff0000u) : (w[i] << 16));
+      const float q0 = mul_rn(x, r);
+      const float zz = fmaf(fmaf(-q0, s, x), r, q0);
+      z[h] = copysignf(fminf(fabsf(zz), 448.0f), x);
+    }
+    const uint32_t two = __builtin_amdgcn_cvt_pk_fp8_f32(z[0], z[1], 0, false) & 0xffffu;
+    out[i >> 1] |= two << ((i & 1) * 16);
+  }
+  return make_uint2(codec_half4(out[0]), codec_half4(out[1]));
+}
+
+__device__ inline float abs_max8(float m, uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bits_f32(w[i] << 16)), fabsf(bits_f32(w[i] & 0xffff0000u))));
+  return m;
+}
+
 inline int64_t packed_weight_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * 16 * K; }
 hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, hipStream_t stream);
 
@@ -176,6 +212,8 @@ hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream);
 // Per-token / per-channel GEMM (a.channel): M <= 16 streams weights (decode
 // shapes), larger M runs the 256 x 256 kernel in its channel form.
 hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream);
+// Per-token quantizer fused into the per-channel decode: a.qa = bf16 x [M][a.ldq], M <= 16.
+hipError_t launch_gemm_token_channel(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream);  // gk_fp8_prefill.hip
 
 // ---- per-token activation quantization (gk_fp8_token.hip) ------------------------

@@ -23,45 +23,11 @@ namespace {
 
 constexpr int kTokThreads = 256;
 
-__device__ inline float token_scale(float m) {  // activation_quant_common.h:3-7
-  const float inv448 = 1.0f / 448.0f;
-  const float s0 = mul_rn(m, inv448);
-  const float res = fmaf(-s0, 448.0f, m);
-  return fmaf(res, inv448, s0);
-}
-
-// 8 bf16 values -> 8 half-range codes (as two packed dwords).
-__device__ inline uint2 token_codes8(uint4 raw, float s, float r) {
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  uint32_t out[2] = {0u, 0u};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float z[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float x = bits_f32(h ? (w[i] & 0xffff0000u) : (w[i] << 16));
-      const float q0 = mul_rn(x, r);
-      const float zz = fmaf(fmaf(-q0, s, x), r, q0);
-      z[h] = copysignf(fminf(fabsf(zz), 448.0f), x);
-    }
-    const uint32_t two = __builtin_amdgcn_cvt_pk_fp8_f32(z[0], z[1], 0, false) & 0xffffu;
-    out[i >> 1] |= two << ((i & 1) * 16);
-  }
-  return make_uint2(codec_half4(out[0]), codec_half4(out[1]));
-}
-
 __device__ inline uint4 token_load8(const uint16_t* xr, int c, int vec_ok) {
   if (vec_ok) return *reinterpret_cast<const uint4*>(xr + c);
   uint32_t h[8];
   for (int j = 0; j < 8; ++j) h[j] = xr[c + j];
   return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-}
-
-__device__ inline float abs_max8(float m, uint4 v) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bits_f32(w[i] << 16)), fabsf(bits_f32(w[i] & 0xffff0000u))));
-  return m;
 }
 
 // One workgroup per row.  Rows of up to kTokKeep * 2048 elements stay in

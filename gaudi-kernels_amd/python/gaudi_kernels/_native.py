@@ -80,6 +80,8 @@ SIGNATURES = {
     "gk_fp8_channel_finish_bf16": (_c_int, [_fp, _c_i64, _c_i64, _c_i64, _fp, _fp, _fp, _c_vp, _c_i64, _c_vp]),
     "gk_fp8_channel_gemm_bf16": (_c_int, [_c_vp, _c_i64, _fp, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _fp, _c_vp,
                                           _c_i64, _c_u32, _c_vp]),
+    "gk_fp8_token_channel_gemm_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _fp, _c_vp,
+                                                _c_i64, _c_u32, _c_vp]),
     "gk_silu_and_mul_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp]),
     "gk_fp8_silu_mul_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _fp, _c_i64, _c_u32, _c_vp]),
     "gk_gelu_and_mul_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_int, _c_vp]),

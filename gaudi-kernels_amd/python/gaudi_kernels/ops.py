@@ -604,3 +604,39 @@ def channel_gemm(q, sa, weight, sw, bias=None, *, out=None):
               nat.load().gk_fp8_channel_gemm_bf16(_ptr(q8), q8.stride(0), _ptr(sa), m, k, _ptr(w8), n, _ptr(sw),
                                                   _ptr(bias), _ptr(y), y.stride(0), 0, _stream(device)))
     return y
+
+
+def token_channel_fused_pays(m, n, k):
+    """Whether the one-launch form (gk_fp8_token_channel_gemm_bf16, up to 16 rows) beats token_quant +
+    channel_gemm.  Every workgroup of the fused form reads its rows' whole activation twice (the token
+    maximum, then the codes), so it pays only for few rows and little redundant work, measured on MI355X
+    (one launch / two): N = 6144, K = 4096: 8.7 / 9.2 us at M <= 4, 10.4 / 10.0 at M = 8; N = 4096,
+    K = 14336: 16.1 / 19.1 us at M <= 4, 22.7 / 19.5 at M = 8; N = 28672, K = 4096: 24.4 / 23.4 us."""
+    return m <= 4 and (-(-n // 32) / 256) * (k / 4096) <= 2.0
+
+
+def token_channel_gemm(x, weight, sw, bias=None, *, out=None, fused=None):
+    """Per-token / per-channel W8A8 on bf16 activations: token_quant then channel_gemm, or both in one
+    launch (gk_fp8_token_channel_gemm_bf16, bit-identical) where token_channel_fused_pays (fused=None) or
+    when fused=True (up to 16 rows; x 16-byte aligned with a row stride that is a multiple of 8)."""
+    device = require_device(x.device)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("expected a 2-D bf16 activation with unit column stride")
+    m, k = x.shape
+    n = _u8(weight).shape[0]
+    if fused is None:
+        fused = token_channel_fused_pays(m, n, k)
+    fused = fused and m <= 16 and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0
+    if not fused:
+        q, sa = token_quant(x)
+        return channel_gemm(q, sa, weight, sw, bias, out=out)
+    w8 = _u8(weight)
+    if w8.shape[1] != k or not w8.is_contiguous():
+        raise ValueError("expected a contiguous weight [N, K]")
+    if sw.shape != (n,) or (bias is not None and bias.shape != (n,)):
+        raise ValueError("expected sw [N] and bias [N]")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=device) if out is None else out
+    nat.check("gk_fp8_token_channel_gemm_bf16",
+              nat.load().gk_fp8_token_channel_gemm_bf16(_ptr(x), x.stride(0), m, k, _ptr(w8), n, _ptr(sw),
+                                                        _ptr(bias), _ptr(y), y.stride(0), 0, _stream(device)))
+    return y

@@ -215,6 +215,18 @@ gk_status gk_fp8_channel_gemm_bf16(const void* q, int64_t ldq, const float* sa, 
                                    int64_t n, const float* sw, const float* bias, void* y, int64_t ldy,
                                    uint32_t flags, void* stream);
 
+/* The per-token quantizer fused into the per-channel GEMM for decode batches
+ * (build-defined; the reference chains three ops: activation_token.c:4-26,
+ * the MME, channel_finish.c:2-18).  x bf16 [m, k] (16-byte aligned, row
+ * stride ldx a multiple of 8, m <= 16, k a multiple of 128); w, sw, bias, y
+ * as gk_fp8_channel_gemm_bf16.  y equals gk_fp8_token_quant_bf16 followed by
+ * gk_fp8_channel_gemm_bf16 bit for bit, in one launch that streams the
+ * weights once.  m > 16 -> GK_INCOMPATIBLE_INPUT_SIZE (call the two ops).
+ * flags must be 0. */
+gk_status gk_fp8_token_channel_gemm_bf16(const void* x, int64_t ldx, int64_t m, int64_t k, const void* w, int64_t n,
+                                         const float* sw, const float* bias, void* y, int64_t ldy, uint32_t flags,
+                                         void* stream);
+
 /* ---- SiLU-and-mul ------------------------------------------------------------ */
 
 /* The reference's gk_silu_and_mul_bf16_v1 (csrc/tpc/generic_dense/

@@ -105,6 +105,22 @@ def test_gemm_rejects_wrong_scale_grid_before_device_use():
     assert st == nat.GK_INCOMPATIBLE_INPUT_SIZE  # m_pad must equal the plan's (16 for decode)
 
 
+def test_token_channel_gemm_rejects_before_device_use():
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)
+    f = lib.gk_fp8_token_channel_gemm_bf16
+    # x, ldx, m, k, w, n, sw, bias, y, ldy, flags, stream
+    assert f(fake, 256, 17, 256, fake, 512, fake, None, fake, 512, 0, None) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert f(fake, 256, 4, 200, fake, 512, fake, None, fake, 512, 0, None) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert f(fake, 128, 4, 256, fake, 512, fake, None, fake, 512, 0, None) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert f(fake, 256, 4, 256, fake, 512, fake, None, fake, 100, 0, None) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE
+    assert f(fake, 260, 4, 256, fake, 512, fake, None, fake, 512, 0, None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+    assert f(ctypes.c_void_p((1 << 20) + 8), 256, 4, 256, fake, 512, fake, None, fake, 512, 0,
+             None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+    assert f(fake, 256, 4, 256, fake, 512, fake, None, fake, 512, 1, None) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
+    assert f(None, 256, 4, 256, fake, 512, fake, None, fake, 512, 0, None) == nat.GK_INVALID_ARGUMENT
+
+
 def test_codec_rejects_before_device_use():
     lib = nat.load()
     fake = ctypes.c_void_p(1 << 20)
@@ -123,3 +139,10 @@ def test_no_gpu_means_loud_failure():
         pytest.skip("GPU present")
     with pytest.raises(RuntimeError):
         ops.require_device()
+
+
+def test_token_channel_fusion_rule():
+    from gaudi_kernels import ops
+    assert ops.token_channel_fused_pays(1, 6144, 4096) and ops.token_channel_fused_pays(4, 4096, 14336)
+    assert not ops.token_channel_fused_pays(8, 6144, 4096)  # M > 4: the redundant quantizer work dominates
+    assert not ops.token_channel_fused_pays(1, 28672, 4096)  # 896 workgroups each reading x twice

@@ -97,3 +97,38 @@ def test_channel_gemm_deterministic_and_rejects():
         ops.channel_gemm(q, sa, w.cuda()[:, :2048], sw.cuda())
     with pytest.raises(Exception):
         ops.token_quant(torch.zeros(4, 100, dtype=torch.bfloat16, device="cuda"))  # width % 128
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 13, 16])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (200, 256), (1000, 768), (4096, 14336), (130, 128)])
+def test_fused_token_channel_equals_two_ops(m, n, k):
+    """gk_fp8_token_channel_gemm_bf16 (one launch) = token quant + channel GEMM, bit for bit."""
+    x = acts(m, k, 31 * m + k).float()
+    if m > 3:
+        x[3] = -0.0  # an all-(-0) token: the zero-row denominator
+        x[0, 5] = 3.0e38 if k > 128 else x[0, 5]  # a huge element
+    x = x.bfloat16().cuda()
+    w, sw = channel_weight(n, k, 40 + n)
+    gen = torch.Generator().manual_seed(41)
+    bias = torch.randn(n, generator=gen).cuda()
+    wd, swd = w.cuda(), sw.cuda()
+    for b in (bias, None):
+        q, sa = ops.token_quant(x)
+        want = ops.channel_gemm(q, sa, wd, swd, b)
+        got = ops.token_channel_gemm(x, wd, swd, b, fused=True)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (m, n, k, b is None)
+
+
+def test_fused_token_channel_strided_and_fallback():
+    x = acts(20, 512, 7)
+    wide = torch.zeros(20, 640, dtype=torch.bfloat16)
+    wide[:, :512] = x
+    xs = wide.cuda()[:, :512]  # row stride 640 elements
+    w, sw = channel_weight(384, 512, 8)
+    wd, swd = w.cuda(), sw.cuda()
+    for m in (1, 16, 20):  # 20 rows: token quant + channel GEMM
+        q, sa = ops.token_quant(xs[:m])
+        want = ops.channel_gemm(q, sa, wd, swd)
+        for fused in (None, True):
+            got = ops.token_channel_gemm(xs[:m], wd, swd, fused=fused)
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (m, fused)
