@@ -65,7 +65,7 @@ def test_encode_dense_sweep_and_specials():
     assert np.array_equal(ours[:-1], theirs[:-1])
 
 
-def test_encode_survey_facts():
+def test_encode_known_codes():
     # torch 2.10 facts the oracle depends on: ties-to-even on the subnormal
     # grid, 464 -> 448, >= 480 -> NaN, 240 -> 0x77, 232 -> 0x76.
     v = np.array([2.0 ** -10, 3 * 2.0 ** -10, 5 * 2.0 ** -10, 464, 480, 240, 232], dtype=np.float32)
