@@ -257,6 +257,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 #pragma unroll
       for (int j = 0; j < 4; ++j) fj[j] = sv[j] * swg;
       load_sav(min(g + 1, gend - 1));
+      asm volatile("" ::: "memory");  // the scale loads stay ahead of the wait, whose count includes them
       // This wave's tile loads of step g are done: vmcnt(8) or vmcnt(4), expcnt(7), lgkmcnt(15).
       if (CH)
         __builtin_amdgcn_s_waitcnt(0x0F74);
