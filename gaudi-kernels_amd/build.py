@@ -27,7 +27,7 @@ OUT_DIR = PKG / "python" / "gaudi_kernels"
 LIB = OUT_DIR / "libgk_fp8.so"
 OBJ_DIR = PKG / "_build"
 SOURCES = ["gk_fp8_codec.hip", "gk_fp8_gemm.hip", "gk_fp8_prefill.hip", "gk_fp8_moe.hip", "gk_fp8_act.hip",
-           "gk_fp8_token.hip", "gk_fp8_norm.hip", "gk_fp8_abi.hip"]
+           "gk_fp8_token.hip", "gk_fp8_norm.hip", "gk_fp8_reduce.hip", "gk_fp8_abi.hip"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

@@ -43,11 +43,17 @@ constexpr const char* kOps[] = {
     "gk_rms_norm_bf16_v1",          // rms_norm_bf16.c, glue generic_dense_glue.cpp:135-190
     "gk_fused_add_rms_norm_bf16_v1",  // fused_add_rms_norm_bf16.c, same glue
     "gk_fp8_rms_norm_quant_bf16_v1",  // (fused add +) RMSNorm fused with the 1x128 quantizer (build-defined)
+    "gk_fp8_block_gemm_kslice_f32_v1",  // K range -> fp32 partial (quant_act_fp16_1k col_offset contract)
+    "gk_rank_sum_f32_v1",           // rank_sum.c, glue generic_dense_glue.cpp:568-600, 871-895
+    "gk_rank_sum_bf16_v1",          // same, bf16 slices
+    "gk_fp8_partial_finish_bf16_v1",  // fp32 partial + bias -> bf16 (reduce_bias.c:42-57 final step)
 };
 constexpr uint32_t kNumOps = sizeof(kOps) / sizeof(kOps[0]);
 
 constexpr uint32_t kKnownFlags = GK_FLAG_NATIVE_HALF | GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL |
                                   GK_FLAG_FORCE_GENERIC | GK_FLAG_WEIGHT_PACKED;
+constexpr uint32_t kKsliceFlags = GK_FLAG_NATIVE_HALF | GK_FLAG_FORCE_DECODE | GK_FLAG_FORCE_PREFILL |
+                                  GK_FLAG_WEIGHT_PACKED | GK_FLAG_ACCUMULATE;
 constexpr size_t kStatusBytes = 256;
 constexpr int64_t kMaxDim = (int64_t{1} << 31) - 1;
 
@@ -180,11 +186,12 @@ bool fused_quant_pays(int64_t m, int64_t n, int64_t k, const gk::DecodeShape& d)
 }
 
 gk_status check_gemm_common(int64_t k, const void* w, int64_t n, const float* scales, int64_t scale_rows,
-                            int64_t scale_cols, const void* y, int64_t ldy) {
+                            int64_t scale_cols, const float* bias, const void* y, int64_t ldy) {
   if (!w || !scales || !y) return GK_INVALID_ARGUMENT;
   if (scale_rows != (n + 127) / 128 || scale_cols != (k + 127) / 128) return GK_INCOMPATIBLE_INPUT_SIZE;
   if (ldy < n) return GK_INCOMPATIBLE_OUTPUT_SIZE;
-  if ((reinterpret_cast<uintptr_t>(scales) & 3) || (reinterpret_cast<uintptr_t>(y) & 1))
+  if (((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(bias)) & 3) ||
+      (reinterpret_cast<uintptr_t>(y) & 1))
     return GK_INCOMPATIBLE_DATA_TYPE;
   return GK_SUCCESS;
 }
@@ -355,7 +362,7 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
   gk_status st = make_plan(m, n, k, flags, w, &p);
   if (st != GK_SUCCESS) return st;
   if (ldx < k) return GK_INCOMPATIBLE_INPUT_SIZE;
-  st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, y, ldy);
+  st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, bias, y, ldy);
   if (st != GK_SUCCESS) return st;
   if (workspace_bytes < p.q_bytes + p.sa_bytes) return GK_INSUFFICIENT_BUFFER;
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) || (reinterpret_cast<uintptr_t>(x) & 1))
@@ -395,7 +402,7 @@ gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, in
   if (st != GK_SUCCESS) return st;
   if (packed && p.variant != GK_VARIANT_DECODE) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
   if (m_pad != p.m_pad) return GK_INCOMPATIBLE_INPUT_SIZE;
-  st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, y, ldy);
+  st = check_gemm_common(k, w, n, scales, scale_rows, scale_cols, bias, y, ldy);
   if (st != GK_SUCCESS) return st;
   if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(sa) & 3))
     return GK_INCOMPATIBLE_DATA_TYPE;
@@ -405,12 +412,138 @@ gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, in
                   static_cast<hipStream_t>(stream));
 }
 
+gk_status gk_fp8_block_gemm_kslice_f32(const void* x, int64_t m, int64_t k, int64_t ldx, int64_t k_offset,
+                                       int64_t k_len, const void* w, int64_t n, const float* scales,
+                                       int64_t scale_rows, int64_t scale_cols, float* partial, int64_t ldp,
+                                       uint32_t flags, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!x || !w || !scales || !partial || !workspace) return GK_INVALID_ARGUMENT;
+  if (flags & ~kKsliceFlags) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  // col_offset rules of generic_fp8_glue.hpp:169-176 (offset >= 0, a multiple of 128) and :245-252 (widths
+  // nonzero multiples of 128, offset + width within the input)
+  if (k_offset < 0 || k_offset % 128) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (m < 1 || n < 1 || k < 128 || k % 128 || k_len < 128 || k_len % 128 || m > kMaxDim || n > kMaxDim ||
+      k > kMaxDim || k_len > k || k_offset > k - k_len || ldx < k)
+    return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (scale_rows != (n + 127) / 128 || scale_cols != k / 128) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldp < n) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(x) & 1) || ((reinterpret_cast<uintptr_t>(scales) |
+                                                 reinterpret_cast<uintptr_t>(partial)) & 3) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const bool wpack = (flags & GK_FLAG_WEIGHT_PACKED) != 0;
+  const int64_t g0 = k_offset / 128, gl = k_len / 128;
+  const uint8_t* wb = static_cast<const uint8_t*>(w) + (wpack ? g0 * 2048 : k_offset);
+  Plan p;
+  gk_status st = make_plan(m, n, k_len, flags & ~uint32_t{GK_FLAG_ACCUMULATE}, wb, &p);
+  if (st != GK_SUCCESS) return st;
+  // the tiled kernels only (the prefill kernel addresses a weight panel of the whole row with 32-bit offsets)
+  if (p.variant == GK_VARIANT_GENERIC || (p.variant == GK_VARIANT_PREFILL && 256 * k > int64_t{0xffffffff}))
+    return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (workspace_bytes < p.q_bytes + p.sa_bytes) return GK_INSUFFICIENT_BUFFER;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* xs = static_cast<const uint16_t*>(x) + k_offset;
+  gk::GemmArgs a{};
+  a.w = wb;
+  a.sw = scales + g0;
+  a.bias = nullptr;
+  a.y = nullptr;
+  a.M = static_cast<int>(m);
+  a.N = static_cast<int>(n);
+  a.K = static_cast<int>(k);  // row stride of the row-major weights
+  a.G = static_cast<int>(gl);
+  a.gs = static_cast<int>(k / 128);
+  a.Mpad = static_cast<int>(p.m_pad);
+  a.half_w = (flags & GK_FLAG_NATIVE_HALF) != 0;
+  a.dec = p.dec;
+  a.wpack = wpack;
+  a.yp = partial;
+  a.ldyp = ldp;
+  a.accumulate = (flags & GK_FLAG_ACCUMULATE) != 0;
+  if (p.variant == GK_VARIANT_DECODE && p.dec.mt == 1 && (reinterpret_cast<uintptr_t>(xs) & 15) == 0 &&
+      ldx % 8 == 0 && fused_quant_pays(m, n, k_len, p.dec)) {
+    a.dec = gk::fused_quant_shape(p.dec, static_cast<int>(gl));
+    a.qa = reinterpret_cast<const uint8_t*>(xs);
+    a.xq = true;
+    a.ldq = ldx;
+    return from_hip(gk::launch_gemm_decode(a, s));
+  }
+  uint8_t* q = static_cast<uint8_t*>(workspace);
+  float* sa = reinterpret_cast<float*>(q + p.q_bytes);
+  const bool packed = p.variant == GK_VARIANT_DECODE;
+  hipError_t e = gk::launch_act_quant(xs, ldx, static_cast<int>(m), static_cast<int>(k_len),
+                                      static_cast<int>(p.m_pad), q, sa, a.half_w, packed, s);
+  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  a.qa = q;
+  a.sa = sa;
+  a.qpack = packed;
+  return from_hip(p.variant == GK_VARIANT_DECODE ? gk::launch_gemm_decode(a, s) : gk::launch_gemm_prefill(a, s));
+}
+
+// ---- row-parallel completion ------------------------------------------------------------
+// infer_rank_sum (generic_dense_glue.cpp:871-895): world_size in [2, 8], the
+// gathered length a nonzero multiple of it.
+gk_status gk_rank_sum_infer(int64_t gathered_elems, int world_size, int64_t* elems) {
+  if (!elems) return GK_INVALID_ARGUMENT;
+  if (world_size < 2 || world_size > 8) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (gathered_elems < world_size || gathered_elems % world_size) return GK_INCOMPATIBLE_INPUT_SIZE;
+  *elems = gathered_elems / world_size;
+  return GK_SUCCESS;
+}
+
+namespace {
+
+// instantiate_rank_sum (generic_dense_glue.cpp:568-600), in its order:
+// world_size, data type (here: alignment), output size, gathered size.
+gk_status rank_sum_common(const void* gathered, int64_t gathered_elems, int world_size, void* dst, int64_t elems,
+                          bool bf16, void* stream) {
+  if (!gathered || !dst) return GK_INVALID_ARGUMENT;
+  if (world_size < 2 || world_size > 8) return GK_UNSUPPORTED_LAYER_CONFIGURATION;
+  if (((reinterpret_cast<uintptr_t>(gathered) | reinterpret_cast<uintptr_t>(dst)) & (bf16 ? 1 : 3)) != 0)
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  if (elems < 1 || elems > kMaxDim / world_size) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (gathered_elems != elems * world_size) return GK_INCOMPATIBLE_INPUT_SIZE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_rank_sum(gathered, dst, elems, world_size, bf16, static_cast<hipStream_t>(stream)));
+}
+
+}  // namespace
+
+gk_status gk_rank_sum_f32(const float* gathered, int64_t gathered_elems, int world_size, float* dst, int64_t elems,
+                          void* stream) {
+  return rank_sum_common(gathered, gathered_elems, world_size, dst, elems, false, stream);
+}
+
+gk_status gk_rank_sum_bf16(const void* gathered, int64_t gathered_elems, int world_size, void* dst, int64_t elems,
+                           void* stream) {
+  return rank_sum_common(gathered, gathered_elems, world_size, dst, elems, true, stream);
+}
+
+gk_status gk_fp8_partial_finish_bf16(const float* partial, int64_t rows, int64_t width, int64_t ldp,
+                                     const float* bias, void* y, int64_t ldy, void* stream) {
+  if (!partial || !y) return GK_INVALID_ARGUMENT;
+  if (rows < 1 || width < 1 || rows > kMaxDim || width > kMaxDim || ldp < width) return GK_INCOMPATIBLE_INPUT_SIZE;
+  if (ldy < width) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if (((reinterpret_cast<uintptr_t>(partial) | reinterpret_cast<uintptr_t>(bias)) & 3) ||
+      (reinterpret_cast<uintptr_t>(y) & 1))
+    return GK_INCOMPATIBLE_DATA_TYPE;
+  const gk_status st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_partial_finish(partial, ldp, static_cast<int>(rows), static_cast<int>(width), bias,
+                                            static_cast<uint16_t*>(y), ldy, static_cast<hipStream_t>(stream)));
+}
+
 gk_status gk_fp8_check_inputs(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
                               const float* scales, int64_t n_scales, void* workspace, size_t workspace_bytes,
                               void* stream) {
   if (!x || !w || !scales || !workspace) return GK_INVALID_ARGUMENT;
   if (m < 1 || k < 1 || n < 1 || ldx < k || n_scales < 1) return GK_INCOMPATIBLE_INPUT_SIZE;
   if (workspace_bytes < kStatusBytes) return GK_INSUFFICIENT_BUFFER;
+  if ((reinterpret_cast<uintptr_t>(x) & 1) || (reinterpret_cast<uintptr_t>(scales) & 3) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 7))
+    return GK_INCOMPATIBLE_DATA_TYPE;
   gk_status st = current_device_ok();
   if (st != GK_SUCCESS) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -731,11 +864,18 @@ gk_status gk_fp8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ld
   if (st != GK_SUCCESS) return st;
   if (ld_logits < E) return GK_INCOMPATIBLE_INPUT_SIZE;
   if (rows_max < rows) return GK_INSUFFICIENT_BUFFER;
+  if (rows_max > kMaxDim) return GK_INCOMPATIBLE_OUTPUT_SIZE;
+  if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(ids) | reinterpret_cast<uintptr_t>(wts) |
+       reinterpret_cast<uintptr_t>(row_of) | reinterpret_cast<uintptr_t>(row_token) |
+       reinterpret_cast<uintptr_t>(offsets)) & 3)
+    return GK_INCOMPATIBLE_DATA_TYPE;
   st = current_device_ok();
   if (st != GK_SUCCESS) return st;
   const gk::MoeRouting r{ids, wts, row_of, row_token, offsets, nullptr};
+  // every entry of the caller's row_token buffer is defined: padding rows and
+  // rows past the layout read -1
   return from_hip(gk::launch_moe_route(logits, static_cast<int>(T), static_cast<int>(E), ld_logits, top_k,
-                                       static_cast<int>(rows), r, static_cast<hipStream_t>(stream)));
+                                       static_cast<int>(rows_max), r, static_cast<hipStream_t>(stream)));
 }
 
 gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, const float* logits, int64_t E,

@@ -93,7 +93,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
                                                               const float* __restrict__ sw,
                                                               const float* __restrict__ bias,
                                                               uint16_t* __restrict__ y, int64_t ldy, int M,
-                                                              int N, int K, int G, int64_t ldq = 0) {
+                                                              int N, int K, int G, int64_t ldq, int gs,
+                                                              float* __restrict__ yp, int64_t ldyp, int accum) {
   static_assert(16 * R <= 128 && NW >= R, "a workgroup's rows lie in one 128-row scale block");
   static_assert(MT == 1 || (!XQ && !CH), "several token tiles take pre-quantized block-scaled activations");
   __shared__ __attribute__((aligned(16))) uint8_t tile[WPACK ? 1 : NW][2048];
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   for (int r = 0; r < R; ++r) {
     if (WPACK) {  // tiles past the last re-read the last tile (never stored)
       const int t = min((n0 >> 4) + r, ((N + 15) >> 4) - 1);
-      wp[r] = w + static_cast<int64_t>(t) * G * 2048 + lane * 16;
+      wp[r] = w + static_cast<int64_t>(t) * gs * 2048 + lane * 16;
       d8[r] = 1024;
     } else {
       const int a0 = min(n0 + 16 * r + lrow, N - 1), a1 = min(n0 + 16 * r + lrow + 8, N - 1);
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
   const int xjn = (min(M, 16) + 3) >> 2;
   constexpr int kQHi = QPACK ? 1024 : 16;
   constexpr int kQG = CH ? 128 : 2048 * MT;         // activation bytes from one group to the next
-  const float* swp = sw + static_cast<int64_t>(n0 >> 7) * G;
+  const float* swp = sw + static_cast<int64_t>(n0 >> 7) * gs;
   const int gbeg = (G * wave) / NW, gend = (G * (wave + 1)) / NW;
   uint8_t* buf = tile[WPACK ? 0 : wave];
 
@@ -309,6 +310,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (n + i < N) row[i] = channel_out(sum[i], sam, sw[n + i], bias ? bias[n + i] : 0.0f);
+    } else if (yp) {  // fp32 partial of this K range (+ the partial already there)
+      if (m >= M) continue;
+      float* row = yp + static_cast<int64_t>(m) * ldyp + n;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n + i < N) row[i] = accum ? row[i] + sum[i] : sum[i];
     } else {
       store_tile(y, ldy, bias, M, N, m, n, sum);
     }
@@ -351,7 +358,8 @@ static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
 #define GK_DECODE_LAUNCH(H, P, WP, X)                                                                          \
   gemm_decode_kernel<NW, R, U, H, P, false, WP, X, MT><<<grid, NW * 64, 0, stream>>>(                               \
-      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq)
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq, a.gstride(), a.yp, a.ldyp,         \
+      a.accumulate ? 1 : 0)
 #define GK_DECODE_LAUNCH_P(H, P, X) \
   if (a.wpack) GK_DECODE_LAUNCH(H, P, true, X); else GK_DECODE_LAUNCH(H, P, false, X)
 #define GK_DECODE_LAUNCH_A(H)                                       \
@@ -369,58 +377,12 @@ static hipError_t decode_launch(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-DecodeShape plan_decode_shape(int N, int G, bool packed_weights, int mt) {
-  // R: 16-row tiles per workgroup.  Every workgroup reads the activations of
-  // its K range once, so larger R cuts activation traffic, but the workgroup
-  // count (tiles / R) must stay near or above the 256 CUs.  NW: waves
-  // splitting K (the partials are summed in wave order, so NW fixes the
-  // result bits; both weight layouts use the same NW for every N and give
-  // identical results).  U: groups per load step, divided by the token tiles
-  // mt (each group's activation fragments grow with mt).  Measured on MI355X
-  // at M = 16 for N x K = 28672 x 4096, 6144 x 4096, 4096 x 14336; the packed
-  // layout (no LDS transpose) gains from the deeper step at N = 6144.
-  (void)G;
-  const int tiles = (N + 15) / 16;
-  DecodeShape d;
-  if (tiles >= 1536) d = DecodeShape{2, 2, 4, 1};
-  else if (tiles >= 384) d = packed_weights ? DecodeShape{8, 2, 4, 1} : DecodeShape{8, 2, 2, 1};
-  else if (tiles >= 256) d = DecodeShape{8, 1, 2, 1};
-  else d = DecodeShape{16, 1, 2, 1};
-  d.mt = mt;
-  d.u = d.u / mt > 0 ? d.u / mt : 1;
-  return d;
-}
-
-DecodeShape fit_group_step(DecodeShape d, int G) {
-  // A wave's last load step is padded with repeats of its last group (loaded
-  // again, multiplied, and scaled by zero), so U is halved until it divides
-  // every wave's group count (G/NW rounded either way).  Measured on MI355X:
-  // 7168 x 7168 (7 groups a wave) 10.9 -> 10.0 us at M = 16 with U = 1,
-  // 8192 x 2048 (2 a wave) 6.5 -> 5.0 us with U = 2.  NW, and so the result
-  // bits, is unchanged.
-  const int lo = G / d.nw, hi = (G + d.nw - 1) / d.nw;
-  while (d.u > 1 && (lo == 0 || lo % d.u != 0 || hi % d.u != 0)) d.u /= 2;
-  return d;
-}
-
-DecodeShape fused_quant_shape(DecodeShape d, int G) {
-  // With the quantizer fused, a load step also quantizes its U groups, and a
-  // padded step repeats that work for nothing.  U divides every wave's group
-  // count: 4 only where each wave has exactly 4 groups, else 2 where both
-  // counts are even, else 1.  More, shorter steps also keep the quantizer's
-  // arithmetic beside the weight fetch.  Measured on MI355X at M = 1, 8, 16
-  // for nine N x K shapes; NW (and so the result bits) is unchanged.
-  const int lo = G / d.nw, hi = (G + d.nw - 1) / d.nw;
-  d.u = (lo == 4 && hi == 4 && d.u == 4) ? 4 : (lo % 2 == 0 && hi % 2 == 0 && lo > 0) ? 2 : 1;
-  return d;
-}
-
 template <int NW, int R, int U, int MT>
 static hipError_t decode_channel_launch(const GemmArgs& a, hipStream_t stream) {
   static_assert(MT == 1, "the per-channel decode takes one token tile");
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
   gemm_decode_kernel<NW, R, U, false, false, true><<<grid, NW * 64, 0, stream>>>(
-      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq);
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq, a.G, nullptr, 0, 0);
   return hipGetLastError();
 }
 
@@ -430,19 +392,9 @@ static hipError_t decode_token_channel_launch(const GemmArgs& a, hipStream_t str
   static_assert(MT == 1, "the fused per-token decode takes one token tile");
   const dim3 grid(static_cast<unsigned>((a.N + 16 * R - 1) / (16 * R)));
   gemm_decode_kernel<NW, R, U, false, false, true, false, true><<<grid, NW * 64, 0, stream>>>(
-      a.qa, nullptr, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq);
+      a.qa, nullptr, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.ldq, a.G, nullptr, 0, 0);
   return hipGetLastError();
 }
-
-// Instantiated decode shapes (NW, R, U, MT); plan_decode_shape and
-// fused_quant_shape return only these (the per-channel decode: the first list).
-#define GK_DECODE_SHAPES1(X) X(2, 2, 4, 1) X(8, 2, 2, 1) X(8, 2, 4, 1) X(8, 1, 2, 1) X(16, 1, 2, 1)
-#define GK_DECODE_SHAPES_T1(X) GK_DECODE_SHAPES1(X) \
-  X(2, 2, 2, 1) X(2, 2, 1, 1) X(8, 2, 1, 1) X(8, 1, 1, 1) X(16, 1, 1, 1)
-#define GK_DECODE_SHAPES(X) GK_DECODE_SHAPES_T1(X)                                             \
-  X(2, 2, 2, 2) X(8, 2, 1, 2) X(8, 2, 2, 2) X(8, 1, 1, 2) X(16, 1, 1, 2)                       \
-  X(2, 2, 1, 4) X(8, 2, 1, 4) X(8, 1, 1, 4) X(16, 1, 1, 4)
-constexpr int decode_key(int nw, int r, int u, int mt) { return ((nw * 10 + r) * 10 + u) * 10 + mt; }
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream) {
   switch (decode_key(a.dec.nw, a.dec.r, a.dec.u, a.dec.mt)) {

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "gk_fp8_math.h"
+#include "gk_fp8_plan.h"
 
 namespace gk {
 
@@ -153,17 +154,6 @@ hipError_t launch_rms_norm(const uint16_t* x, const uint16_t* res, int64_t ld_in
                            int width, float eps, float off, uint16_t* res_out, uint16_t* norm_out, int64_t ld_out,
                            uint8_t* q, float* sa, int Mpad, bool half, bool packed, hipStream_t stream);
 
-// Decode variant shape: NW waves per workgroup (splitting K), R 16-row weight
-// tiles per workgroup, U groups per load step.  Chosen by plan_decode_shape.
-struct DecodeShape {
-  int nw, r, u, mt;  // mt: 16-token column tiles
-};
-DecodeShape plan_decode_shape(int N, int G, bool packed_weights, int mt);
-// U reduced to divide every wave's group count (no padded load steps).
-DecodeShape fit_group_step(DecodeShape d, int G);
-// The shape of the decode kernel with the quantizer fused (XQ, one token tile).
-DecodeShape fused_quant_shape(DecodeShape d, int G);
-
 // Quantized activations qa [G][Mpad][128] / sa [G][Mpad] (launch_act_quant)
 // times weight codes w [N, K] with block scales sw [ceil(N/128), G].
 struct GemmArgs {
@@ -189,6 +179,18 @@ struct GemmArgs {
   // Decode variant only: qa is the bf16 activation x [M][ldq] (16-byte
   // aligned rows, ldq % 8 == 0), quantized inside the GEMM (sa unused).
   bool xq = false;
+  // K range of a larger weight (decode and 256 x 256 kernels, block scaling):
+  // w and sw already point at the range's first group, G counts its groups,
+  // K stays the weight row stride and gs the groups of the whole row (the
+  // scale-grid row stride and, for packed weights, the 16-row tile stride in
+  // 2 KB blocks).  0: the whole row (gs = G).
+  int gs = 0;
+  int gstride() const { return gs > 0 ? gs : G; }
+  // fp32 output instead of bf16 y: yp [M][ldyp] = the sum over the K range
+  // (+ yp when accumulate), no bias.
+  float* yp = nullptr;
+  int64_t ldyp = 0;
+  bool accumulate = false;
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
@@ -215,6 +217,14 @@ hipError_t launch_gemm_channel(const GemmArgs& a, hipStream_t stream);
 // Per-token quantizer fused into the per-channel decode: a.qa = bf16 x [M][a.ldq], M <= 16.
 hipError_t launch_gemm_token_channel(const GemmArgs& a, hipStream_t stream);
 hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream);  // gk_fp8_prefill.hip
+
+// ---- row-parallel completion (gk_fp8_reduce.hip) -------------------------------------
+// rank_sum.c:4-42: dst[i] = sum over r < world of gathered[r * elems + i] in
+// fp32, rank order (bf16: slices widened, one final bf16 rounding).
+hipError_t launch_rank_sum(const void* gathered, void* dst, int64_t elems, int world, bool bf16, hipStream_t stream);
+// y = bf16(p + bias) on an fp32 partial [rows][width] (bias may be null).
+hipError_t launch_partial_finish(const float* p, int64_t ldp, int rows, int width, const float* bias, uint16_t* y,
+                                 int64_t ldy, hipStream_t stream);
 
 // ---- per-token activation quantization (gk_fp8_token.hip) ------------------------
 // activation_token.c:4-26: q [rows][width] Gaudi2 half-range codes (row-major,

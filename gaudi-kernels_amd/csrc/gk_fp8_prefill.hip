@@ -85,8 +85,13 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
 // has the matrix core to itself.
 //
 // fp32 output (yp != nullptr): the tile stores fp32 sums to yp[part][m][n]
-// instead of bf16 y (no bias).  K split (kparts = 2, grid doubled, needs yp):
-// the second half of the grid takes the second half of the groups.
+// (row stride ldyp, plane stride M * ldyp) instead of bf16 y (no bias).  K
+// split (kparts = 2, grid doubled, needs yp): the second half of the grid
+// takes the second half of the groups.  accum: the sums start from yp.
+//
+// K range (gs > G): w and sw point at the range's first group; gs is the
+// groups of the whole weight row (scale row stride, packed tile stride in
+// 2 KB blocks) while K stays the row-major weight row stride.
 //
 // CH (per-token / per-channel scaling): activations row-major [M][ldq] (rows
 // past M re-read row M-1), sa [M], sw [N]; the MFMAs accumulate over all of
@@ -110,7 +115,8 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
                                                               const int32_t* __restrict__ group_off,
                                                               const int32_t* __restrict__ group_cnt, int n_groups,
                                                               int64_t w_stride, int64_t sw_stride, int kparts,
-                                                              float* __restrict__ yp, int64_t ldq = 0) {
+                                                              float* __restrict__ yp, int64_t ldq, int gs,
+                                                              int64_t ldyp, int accum) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
@@ -180,7 +186,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
       if (WPACK) {  // block 2 wave + i/2 of the tile (blocks past the last re-read the last one), half i % 2
         const int blk = min(2 * wave + (i >> 1), nblk);
         vo = lane16;
-        so = static_cast<uint32_t>((blk * G + g) * 2048 + (i & 1) * 1024);
+        so = static_cast<uint32_t>((blk * gs + g) * 2048 + (i & 1) * 1024);
       } else {
         vo = aoff[i];
         so = static_cast<uint32_t>(g) * 128u;
@@ -217,8 +223,13 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const uint32_t lbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
   const uint32_t arow = WPACK ? pa : (wn * 64 + fr) * 128, brow = kWStages * kTile + (wm * 128 + fr) * 128;
   const float* sap = sa + (m0 + wm * 128 + fr);  // + 32 j + g * Mpad  (m0 + 256 <= Mpad)
-  const float* swp = sw + static_cast<int64_t>(min(n0 + wn * 64, N - 1) >> 7) * G;
+  const float* swp = sw + static_cast<int64_t>(min(n0 + wn * 64, N - 1) >> 7) * gs;
+  float* ypp = yp ? yp + static_cast<int64_t>(part) * M * ldyp : nullptr;
 
+  // Accumulator element (i, j, 4 q + r) is output (m0 + wm*128 + 32 j + fr,
+  // n0 + wn*64 + 32 i + 8 q + 4 (lane/32) + r).  With accum the sums start
+  // from the fp32 partial in yp, so K ranges accumulated over several calls
+  // give the bits of one call over their union.
   v16f acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -226,6 +237,22 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  if (accum) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + wm * 128 + j * 32 + fr;
+        if (j >= jlive || m >= M) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < N) acc[i][j][4 * q + r] = ypp[static_cast<int64_t>(m) * ldyp + n + r];
+        }
+      }
+  }
 
   // Issue order in step g: token scales of g + 1 (before the wait), then, past
   // the barrier, activations of g + 1 and weights of g + 2.  Weights are issued
@@ -337,7 +364,6 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     return;
   }
   if (yp) {
-    float* ypp = yp + static_cast<int64_t>(part) * M * N;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -346,9 +372,16 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int m = m0 + wm * 128 + j * 32 + fr, n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-            if (m < M && n < N)  // N % 4 == 0 here
-              *reinterpret_cast<v4f*>(ypp + static_cast<int64_t>(m) * N + n) =
-                  v4f{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            if (m >= M) continue;
+            float* dst = ypp + static_cast<int64_t>(m) * ldyp + n;
+            const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            if (n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+              *reinterpret_cast<v4f*>(dst) = v;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (n + r < N) dst[r] = v[r];
+            }
           }
         }
       }
@@ -392,13 +425,13 @@ hipError_t ensure_lds_limit() {
 
 template <bool HALF, bool GROUPED, bool WPACK = false>
 hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
-                     int64_t w_stride, int64_t sw_stride, int kparts, float* yp, hipStream_t stream) {
+                     int64_t w_stride, int64_t sw_stride, int kparts, float* yp, int64_t ldyp, hipStream_t stream) {
   hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK>();
   if (e != hipSuccess) return e;
   const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
   gemm_prefill256_kernel<HALF, GROUPED, false, WPACK><<<tiles * kparts, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
-      w_stride, sw_stride, kparts, yp);
+      w_stride, sw_stride, kparts, yp, 0, a.gstride(), ldyp, a.accumulate ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -414,7 +447,7 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
   const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (mpad / kBM));
   gemm_prefill256_kernel<false, false, true><<<tiles, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, mpad, nullptr, nullptr, 0, 0, 0, 1, nullptr,
-      a.ldq);
+      a.ldq, a.G, 0, 0);
   return hipGetLastError();
 }
 
@@ -423,10 +456,10 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
   if (a.Mpad % kBM != 0 || !prefill256_fits(a)) return hipErrorInvalidValue;
   if (a.wpack)
-    return a.half_w ? launch256<true, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream)
-                    : launch256<false, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream);
-  return a.half_w ? launch256<true, false>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream)
-                  : launch256<false, false>(a, nullptr, nullptr, 0, 0, 0, 1, nullptr, stream);
+    return a.half_w ? launch256<true, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
+                    : launch256<false, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
+  return a.half_w ? launch256<true, false>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
+                  : launch256<false, false>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
 }
 
 // Grouped form: a.Mpad = padded rows (multiple of 256), a.M = a.Mpad; weights
@@ -441,12 +474,13 @@ hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, c
   const int64_t w_stride = a.wpack ? packed_weight_bytes(a.N, a.K) : static_cast<int64_t>(a.N) * a.K;
   const int64_t sw_stride = static_cast<int64_t>((a.N + 127) / 128) * a.G;
   if (a.wpack)
-    return a.half_w
-               ? launch256<true, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, stream)
-               : launch256<false, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
-                                              stream);
-  return a.half_w ? launch256<true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, stream)
-                  : launch256<false, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
+    return a.half_w ? launch256<true, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
+                                                  a.N, stream)
+                    : launch256<false, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts,
+                                                   yp, a.N, stream);
+  return a.half_w ? launch256<true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, a.N,
+                                          stream)
+                  : launch256<false, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp, a.N,
                                            stream);
 }
 

@@ -44,6 +44,7 @@ GK_FLAG_FORCE_PREFILL = 4
 GK_FLAG_FORCE_GENERIC = 8
 GK_FLAG_DECODE_LAYOUT = 16
 GK_FLAG_WEIGHT_PACKED = 32
+GK_FLAG_ACCUMULATE = 64
 
 GK_VARIANT_DECODE = 1
 GK_VARIANT_PREFILL = 2
@@ -74,6 +75,12 @@ SIGNATURES = {
                                         _c_vp, _c_i64, _c_u32, _c_vp, _c_size, _c_vp]),
     "gk_fp8_block_gemm_q_bf16": (_c_int, [_c_vp, _fp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _c_i64, _c_i64,
                                           _fp, _c_vp, _c_i64, _c_u32, _c_vp]),
+    "gk_fp8_block_gemm_kslice_f32": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp,
+                                              _c_i64, _c_i64, _fp, _c_i64, _c_u32, _c_vp, _c_size, _c_vp]),
+    "gk_fp8_partial_finish_bf16": (_c_int, [_fp, _c_i64, _c_i64, _c_i64, _fp, _c_vp, _c_i64, _c_vp]),
+    "gk_rank_sum_f32": (_c_int, [_fp, _c_i64, _c_int, _fp, _c_i64, _c_vp]),
+    "gk_rank_sum_bf16": (_c_int, [_c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_vp]),
+    "gk_rank_sum_infer": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_i64)]),
     "gk_fp8_check_inputs": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _c_i64, _c_vp, _c_size,
                                      _c_vp]),
     "gk_fp8_token_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _c_vp]),

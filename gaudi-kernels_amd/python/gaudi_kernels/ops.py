@@ -640,3 +640,93 @@ def token_channel_gemm(x, weight, sw, bias=None, *, out=None, fused=None):
               nat.load().gk_fp8_token_channel_gemm_bf16(_ptr(x), x.stride(0), m, k, _ptr(w8), n, _ptr(sw),
                                                         _ptr(bias), _ptr(y), y.stride(0), 0, _stream(device)))
     return y
+
+
+# ---- K ranges and the row-parallel completion ---------------------------------------------
+
+
+def block_fp8_gemm_kslice(x, weight, scales, k_offset, k_len, *, native_half=False, variant=None, out=None,
+                          accumulate=False, workspace=None):
+    """fp32 partial of the block-FP8 GEMM over the K columns [k_offset, k_offset + k_len) (asynchronous).
+
+    x bf16 [M, K], weight [N, K] (row-major codes or a PackedWeight), scales the whole
+    [ceil(N/128), K/128] grid.  Returns out fp32 [M, N] (allocated when None) holding
+    sum_g P_g * sa * sw over the range's groups, added to out's contents when accumulate=True
+    (the reference's chunked prefill chain carries c0 over K chunks this way,
+    fp8_hybrid_tpcsim_test.cpp:253-302).  k_offset and k_len: multiples of 128 inside K
+    (generic_fp8_glue.hpp:169-176, :245-252).  variant: None, "decode" or "prefill".
+    """
+    device = require_device(x.device)
+    if x.dtype != torch.bfloat16 or x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("expected a 2-D bf16 activation with unit column stride")
+    _check_gemm_operands(weight, scales, None, device)
+    m, k = x.shape
+    w8, n, kw, wflag = _weight_args(weight)
+    if kw != k:
+        raise ValueError("activation and weight K differ")
+    if variant == "generic":
+        raise ValueError("the K-range GEMM runs the decode or the LDS-tiled variant")
+    flags = _flags(native_half, variant) | wflag
+    _, _, ws_bytes = plan(m, n, max(128, int(k_len)), flags, w8)
+    ws = _checked_workspace(workspace, ws_bytes, device)
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate=True needs the partial to add to (out)")
+        out = torch.empty((m, n), dtype=torch.float32, device=device)
+    elif out.dtype != torch.float32 or out.shape != (m, n) or out.stride(1) != 1 or out.device != device:
+        raise ValueError("out must be fp32 [M, N] with unit column stride on the same GPU")
+    if accumulate:
+        flags |= nat.GK_FLAG_ACCUMULATE
+    lib = nat.load()
+    nat.check("gk_fp8_block_gemm_kslice_f32",
+              lib.gk_fp8_block_gemm_kslice_f32(_ptr(x), m, k, x.stride(0), int(k_offset), int(k_len), _ptr(w8), n,
+                                               _ptr(scales), scales.shape[0], scales.shape[1], _ptr(out),
+                                               out.stride(0), flags, _ptr(ws), ws.numel(), _stream(device)))
+    return out
+
+
+def partial_finish(partial, bias=None, *, out=None):
+    """bf16(partial + bias) of an fp32 partial [rows, width] (the decode reduce's last step, reduce_bias.c:42-57)."""
+    device = require_device(partial.device)
+    if partial.dtype != torch.float32 or partial.ndim != 2 or partial.stride(1) != 1:
+        raise ValueError("expected a 2-D fp32 partial with unit column stride")
+    rows, width = partial.shape
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != width
+                             or bias.device != device):
+        raise ValueError("expected a contiguous fp32 bias with `width` elements on the same GPU")
+    if out is None:
+        out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    lib = nat.load()
+    nat.check("gk_fp8_partial_finish_bf16",
+              lib.gk_fp8_partial_finish_bf16(_ptr(partial), rows, width, partial.stride(0), _ptr(bias), _ptr(out),
+                                             out.stride(0), _stream(device)))
+    return out
+
+
+def rank_sum_infer(gathered_elems, world_size):
+    """Slice length of a gathered buffer (infer_rank_sum, generic_dense_glue.cpp:871-895)."""
+    elems = ctypes.c_int64(0)
+    nat.check("gk_rank_sum_infer", nat.load().gk_rank_sum_infer(int(gathered_elems), int(world_size),
+                                                                 ctypes.byref(elems)))
+    return elems.value
+
+
+def rank_sum(gathered, world_size, *, out=None):
+    """Ordered sum of world_size contiguous slices of a 1-D fp32 or bf16 buffer (rank_sum.c:4-42).
+
+    gathered: [world_size * elems] (what an all-gather of the ranks' slices leaves).  Returns
+    [elems] of the same dtype: ((s_0 + s_1) + s_2) + ... in fp32, one bf16 rounding for bf16.
+    """
+    device = require_device(gathered.device)
+    if gathered.ndim != 1 or not gathered.is_contiguous() or gathered.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("expected a contiguous 1-D fp32 or bf16 gathered buffer")
+    elems = rank_sum_infer(gathered.numel(), world_size)
+    if out is None:
+        out = torch.empty(elems, dtype=gathered.dtype, device=device)
+    elif out.dtype != gathered.dtype or out.numel() != elems or not out.is_contiguous() or out.device != device:
+        raise ValueError("out must be a contiguous [elems] buffer of the gathered dtype")
+    lib = nat.load()
+    fn = lib.gk_rank_sum_f32 if gathered.dtype == torch.float32 else lib.gk_rank_sum_bf16
+    nat.check(fn.__name__, fn(_ptr(gathered), gathered.numel(), int(world_size), _ptr(out), elems,
+                              _stream(device)))
+    return out

@@ -61,6 +61,7 @@ typedef enum gk_status {
 #define GK_FLAG_FORCE_GENERIC 8u   /* force the any-shape variant */
 #define GK_FLAG_DECODE_LAYOUT 16u  /* act_quant / q GEMM only: quantized activations in the decode fragment layout */
 #define GK_FLAG_WEIGHT_PACKED 32u  /* block GEMMs, MoE layer: weights packed by gk_fp8_pack_weight (not the generic variant) */
+#define GK_FLAG_ACCUMULATE 64u     /* K-slice GEMM only: add into the fp32 partial instead of overwriting it */
 
 /* Variants reported by gk_fp8_block_gemm_plan. */
 #define GK_VARIANT_DECODE 1
@@ -173,6 +174,68 @@ gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, in
                                    const void* w, int64_t n, const float* scales, int64_t scale_rows,
                                    int64_t scale_cols, const float* bias, void* y, int64_t ldy, uint32_t flags,
                                    void* stream);
+
+/* One K range of the block-FP8 GEMM, as an fp32 partial: the chunked-K form
+ * of the reference's prefill chain, whose activation quantizer takes a
+ * col_offset (gk_fp8_quant_act_fp16_1k_v1, generic_fp8_glue.hpp:233-273;
+ * fp8_hybrid_tpcsim_test.cpp:253-302 accumulates c0 over K chunks), and the
+ * per-shard GEMM of a row-parallel (K-sharded) linear layer.
+ *   partial[i][j] (+)= sum over groups g in [k_offset/128, (k_offset+k_len)/128)
+ *                      of P_g[i][j] * sa[i][g] * sw[j/128][g]
+ * x bf16 [m, k] (row stride ldx; only columns [k_offset, k_offset + k_len)
+ * are read), w codes [n, k] (row-major, or packed for (n, k) with
+ * GK_FLAG_WEIGHT_PACKED), scales the whole [ceil(n/128), k/128] grid,
+ * partial fp32 [m, n] (row stride ldp).  The activation groups of the range
+ * are quantized exactly as in gk_fp8_block_gemm_bf16.  GK_FLAG_ACCUMULATE adds
+ * the range's sum to what partial holds.  No bias; finish with
+ * gk_fp8_partial_finish_bf16 (directly, or after gk_rank_sum_f32 over the
+ * shards' partials).
+ * Rules (the col_offset rules of generic_fp8_glue.hpp:169-176, :245-252):
+ * k_offset < 0 or not a multiple of 128 -> GK_UNSUPPORTED_LAYER_CONFIGURATION;
+ * k or k_len not a nonzero multiple of 128, or k_offset + k_len > k (e.g.
+ * offset 384 + 256 > 512, generic_fp8_glue_test.cpp:216-218) ->
+ * GK_INCOMPATIBLE_INPUT_SIZE.  The workspace is gk_fp8_block_gemm_plan(m, n,
+ * k_len, flags, w) bytes; the variant is that plan's (decode for m <= 64, the
+ * LDS-tiled kernel above; the generic variant is not offered here).  On the
+ * LDS-tiled kernel the sums start from partial when accumulating, so
+ * consecutive ranges accumulated over several calls give the bits of one call
+ * over their union; the decode kernel splits each range over its waves, so
+ * there the bits depend on the ranges (each call within the GEMM gate). */
+gk_status gk_fp8_block_gemm_kslice_f32(const void* x, int64_t m, int64_t k, int64_t ldx, int64_t k_offset,
+                                       int64_t k_len, const void* w, int64_t n, const float* scales,
+                                       int64_t scale_rows, int64_t scale_cols, float* partial, int64_t ldp,
+                                       uint32_t flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* y[i][j] = bf16(partial[i][j] + bias[j]) (one fp32 addition, one rounding to
+ * nearest even; bias may be NULL): the final step of the decode reduce
+ * (csrc/tpc/block_fp8_framework/reduce_bias.c:42-57) on an fp32 partial
+ * [rows, width] (row stride ldp) -> bf16 [rows, width] (row stride ldy). */
+gk_status gk_fp8_partial_finish_bf16(const float* partial, int64_t rows, int64_t width, int64_t ldp,
+                                     const float* bias, void* y, int64_t ldy, void* stream);
+
+/* ---- row-parallel rank sum ------------------------------------------------------ */
+
+/* The reference's gk_rank_sum_f32_v1 / gk_rank_sum_bf16_v1
+ * (csrc/tpc/generic_dense/rank_sum.c:4-42, glue generic_dense_glue.cpp:568-600):
+ * gathered holds world_size contiguous slices of `elems` values (slice r at
+ * r * elems, as an all-gather leaves them); dst[i] = ((s_0[i] + s_1[i]) +
+ * s_2[i]) + ... in fp32, in rank order.  The bf16 form widens each slice,
+ * sums the same way and rounds once to bf16 (nearest even).  Checks, in the
+ * glue's order: world_size outside [2, 8] ->
+ * GK_UNSUPPORTED_LAYER_CONFIGURATION; misaligned buffers ->
+ * GK_INCOMPATIBLE_DATA_TYPE; elems < 1 or elems * world_size beyond int32 ->
+ * GK_INCOMPATIBLE_OUTPUT_SIZE; gathered_elems != elems * world_size ->
+ * GK_INCOMPATIBLE_INPUT_SIZE.  Stream-ordered. */
+gk_status gk_rank_sum_f32(const float* gathered, int64_t gathered_elems, int world_size, float* dst, int64_t elems,
+                          void* stream);
+gk_status gk_rank_sum_bf16(const void* gathered, int64_t gathered_elems, int world_size, void* dst, int64_t elems,
+                           void* stream);
+
+/* Shape inference of the rank sum (infer_rank_sum, generic_dense_glue.cpp:871-895):
+ * *elems = gathered_elems / world_size; world_size outside [2, 8] ->
+ * GK_UNSUPPORTED_LAYER_CONFIGURATION; gathered_elems < world_size or not a
+ * multiple of it -> GK_INCOMPATIBLE_INPUT_SIZE. */
+gk_status gk_rank_sum_infer(int64_t gathered_elems, int world_size, int64_t* elems);
 
 /* Finite-input check of block_fp8_oracle.py:22-24 on device buffers: every
  * activation finite, no OCP NaN weight code, every scale finite and >= 0.
@@ -325,8 +388,11 @@ gk_status gk_fp8_moe_rows_max(int64_t T, int64_t E, int top_k, int64_t* rows_max
 gk_status gk_fp8_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, size_t* bytes);
 
 /* Routing only: ids int32 [T, k], wts fp32 [T, k], row_of int32 [T, k]
- * (padded row of each slot), row_token int32 [rows_max] (-1 = padding),
- * offsets int32 [E + 1] (padded segment starts; offsets[E] = rows in use). */
+ * (padded row of each slot), row_token int32 [rows_max] (every entry is
+ * written: the token of each routed row, -1 for padding rows and for rows at
+ * or past offsets[E]), offsets int32 [E + 1] (padded segment starts;
+ * offsets[E] = rows in use).  rows_max below gk_fp8_moe_rows_max ->
+ * GK_INSUFFICIENT_BUFFER; every buffer 4-byte aligned. */
 gk_status gk_fp8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ld_logits, int top_k, int32_t* ids,
                            float* wts, int32_t* row_of, int32_t* row_token, int64_t rows_max, int32_t* offsets,
                            void* stream);

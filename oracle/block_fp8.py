@@ -94,6 +94,15 @@ def act_quant_bits(x_f32, native_half=False):
 
 def reference(x, weight, scales, *, native_half=False, bias=None, row_chunk=64):
     """Row-batched restatement of ``block_fp8_oracle.reference`` (M >= 1). Returns bf16 [M, N]."""
+    return _reference(x, weight, scales, native_half, bias, row_chunk, torch.bfloat16)
+
+
+def reference_f64(x, weight, scales, *, native_half=False, row_chunk=64):
+    """The same sum in fp64 before the final rounding (block_fp8_oracle.py:38-41, no bias) -> fp64 [M, N]."""
+    return _reference(x, weight, scales, native_half, None, row_chunk, torch.float64)
+
+
+def _reference(x, weight, scales, native_half, bias, row_chunk, out_dtype):
     n, k, groups = validate(x, weight, scales, bias)
     m = x.shape[0]
     qa, sa = act_quant(x, native_half)
@@ -106,7 +115,7 @@ def reference(x, weight, scales, *, native_half=False, bias=None, row_chunk=64):
     wg = w.reshape(n, groups, 128).permute(1, 2, 0).double()          # [G, 128, N], once per call
     sw = scales.repeat_interleave(128, dim=0)[:n].T.double()           # [G, N]
     bias64 = bias.double().reshape(1, n) if bias is not None else None
-    out = torch.empty((m, n), dtype=torch.bfloat16)
+    out = torch.empty((m, n), dtype=out_dtype)
     for r0 in range(0, m, row_chunk):
         r1 = min(m, r0 + row_chunk)
         qc = qa[r0:r1].permute(1, 0, 2).double()                        # [G, rows, 128]
@@ -115,7 +124,7 @@ def reference(x, weight, scales, *, native_half=False, bias=None, row_chunk=64):
         y = (partial * sac * sw.unsqueeze(1)).sum(0)                     # [rows, N]
         if bias64 is not None:
             y = y + bias64
-        out[r0:r1] = y.to(torch.bfloat16)
+        out[r0:r1] = y.to(out_dtype)
     return out
 
 

@@ -146,3 +146,96 @@ def test_token_channel_fusion_rule():
     assert ops.token_channel_fused_pays(1, 6144, 4096) and ops.token_channel_fused_pays(4, 4096, 14336)
     assert not ops.token_channel_fused_pays(8, 6144, 4096)  # M > 4: the redundant quantizer work dominates
     assert not ops.token_channel_fused_pays(1, 28672, 4096)  # 896 workgroups each reading x twice
+
+
+def test_alignment_rejections_before_device_use():
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)
+    ws = ctypes.c_void_p(1 << 21)
+    odd4 = ctypes.c_void_p((1 << 20) + 2)  # 2-byte aligned: not an fp32 buffer
+    odd2 = ctypes.c_void_p((1 << 20) + 1)
+    # a misaligned fp32 bias, as the channel GEMM and channel finish reject it
+    st = lib.gk_fp8_block_gemm_bf16(fake, 4, 256, 256, fake, 512, fake, 4, 2, odd4, fake, 512, 0, ws, 1 << 20, None)
+    assert st == nat.GK_INCOMPATIBLE_DATA_TYPE
+    st = lib.gk_fp8_block_gemm_q_bf16(fake, fake, 4, 16, 256, fake, 512, fake, 4, 2, odd4, fake, 512, 0, None)
+    assert st == nat.GK_INCOMPATIBLE_DATA_TYPE
+    # the finite-input check: bf16 x, fp32 scales, the status workspace
+    f = lib.gk_fp8_check_inputs
+    assert f(odd2, 4, 256, 256, fake, 512, fake, 8, ws, 256, None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+    assert f(fake, 4, 256, 256, fake, 512, odd4, 8, ws, 256, None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+    assert f(fake, 4, 256, 256, fake, 512, fake, 8, ctypes.c_void_p((1 << 21) + 4), 256,
+             None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+
+
+def test_moe_route_rejections_before_device_use():
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)
+    rows = ctypes.c_int64(0)
+    assert lib.gk_fp8_moe_rows_max(512, 8, 2, ctypes.byref(rows)) == nat.GK_SUCCESS
+    f = lib.gk_fp8_moe_route
+    # logits, T, E, ld, k, ids, wts, row_of, row_token, rows_max, offsets, stream
+    assert f(fake, 512, 8, 8, 2, fake, fake, fake, fake, rows.value - 1, fake, None) == nat.GK_INSUFFICIENT_BUFFER
+    assert f(fake, 512, 8, 8, 2, fake, fake, fake, fake, 1 << 40, fake, None) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE
+    assert f(fake, 512, 8, 8, 2, fake, fake, fake, ctypes.c_void_p((1 << 20) + 2), rows.value, fake,
+             None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+
+
+def test_rank_sum_rejections_before_device_use():
+    """generic_dense_glue_contract_test.cpp:533-584 and the glue's checks (generic_dense_glue.cpp:568-600, 871-895)."""
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)
+    elems = ctypes.c_int64(0)
+    assert lib.gk_rank_sum_infer(16384, 4, ctypes.byref(elems)) == nat.GK_SUCCESS and elems.value == 4096
+    for bad in (1, 9):
+        assert lib.gk_rank_sum_infer(16384, bad, ctypes.byref(elems)) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
+    assert lib.gk_rank_sum_infer(3, 4, ctypes.byref(elems)) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert lib.gk_rank_sum_infer(10, 4, ctypes.byref(elems)) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    for fn in (lib.gk_rank_sum_f32, lib.gk_rank_sum_bf16):
+        assert fn(fake, 16384, 1, fake, 4096, None) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
+        assert fn(fake, 16384, 9, fake, 4096, None) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
+        assert fn(fake, 8192, 4, fake, 4096, None) == nat.GK_INCOMPATIBLE_INPUT_SIZE   # mismatched gathered size
+        assert fn(fake, 0, 4, fake, 0, None) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE
+        assert fn(fake, 4 << 30, 4, fake, 1 << 30, None) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE  # beyond int32
+        assert fn(None, 16384, 4, fake, 4096, None) == nat.GK_INVALID_ARGUMENT
+    assert lib.gk_rank_sum_f32(ctypes.c_void_p((1 << 20) + 2), 16384, 4, fake, 4096,
+                               None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+    assert lib.gk_rank_sum_bf16(ctypes.c_void_p((1 << 20) + 1), 16384, 4, fake, 4096,
+                                None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+
+
+def test_kslice_col_offset_rules_before_device_use():
+    """The col_offset contract of generic_fp8_glue.hpp:169-176, :245-252 and generic_fp8_glue_test.cpp:196-220."""
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)
+    ws = ctypes.c_void_p(1 << 21)
+    f = lib.gk_fp8_block_gemm_kslice_f32
+    # x, m, k, ldx, k_offset, k_len, w, n, scales, rows, cols, partial, ldp, flags, ws, ws_bytes, stream
+
+    def call(k_offset, k_len, k=512, flags=0, ldp=256, ws_bytes=1 << 20, rows=2, cols=None):
+        return f(fake, 4, k, k, k_offset, k_len, fake, 256, fake, rows, k // 128 if cols is None else cols, fake, ldp,
+                 flags, ws, ws_bytes, None)
+
+    # offset 384 + 256 > 512: rejected as an input size (generic_fp8_glue_test.cpp:216-218)
+    assert call(384, 256) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert call(100, 256) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION     # not a multiple of 128
+    assert call(-128, 256) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
+    assert call(0, 0) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert call(0, 200) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert call(0, 256, k=500) == nat.GK_INCOMPATIBLE_INPUT_SIZE         # K itself a multiple of 128
+    assert call(256, 256, cols=2) == nat.GK_INCOMPATIBLE_INPUT_SIZE      # the whole-K scale grid
+    assert call(256, 256, ldp=100) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE
+    assert call(256, 256, ws_bytes=16) == nat.GK_INSUFFICIENT_BUFFER
+    assert call(256, 256, flags=nat.GK_FLAG_FORCE_GENERIC) == nat.GK_UNSUPPORTED_LAYER_CONFIGURATION
+    assert f(fake, 4, 512, 512, 256, 256, fake, 256, fake, 2, 4, ctypes.c_void_p((1 << 20) + 2), 256, 0, ws, 1 << 20,
+             None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+
+
+def test_partial_finish_rejections_before_device_use():
+    lib = nat.load()
+    fake = ctypes.c_void_p(1 << 20)
+    f = lib.gk_fp8_partial_finish_bf16
+    assert f(fake, 0, 16, 16, None, fake, 16, None) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert f(fake, 2, 16, 8, None, fake, 16, None) == nat.GK_INCOMPATIBLE_INPUT_SIZE
+    assert f(fake, 2, 16, 16, None, fake, 8, None) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE
+    assert f(fake, 2, 16, 16, ctypes.c_void_p((1 << 20) + 2), fake, 16, None) == nat.GK_INCOMPATIBLE_DATA_TYPE
+    assert f(None, 2, 16, 16, None, fake, 16, None) == nat.GK_INVALID_ARGUMENT

@@ -197,3 +197,18 @@ def test_decode_strided_unaligned_activations(native_half, m):
     y_dense = ops.block_fp8_gemm(x.cuda(), w.cuda(), s.cuda(), native_half=native_half, variant="decode")
     assert torch.equal(y_strided.view(torch.int16), y_dense.view(torch.int16))
     assert_parity(y_dense.cpu(), block_fp8.reference(x, w, s, native_half=native_half))
+
+
+@pytest.mark.parametrize("m,n,k", [(20, 24576, 2304), (32, 28672, 384)])
+def test_decode_two_tile_narrow_step_shape(m, n, k):
+    """Wide N (>= 1536 row tiles) with two token tiles and an odd group count per wave: the planner's
+    (NW=2, R=2, U=1, MT=2) shape, for row-major and packed weights (bit-identical to each other)."""
+    assert ops.plan(m, n, k)[0] == 1  # GK_VARIANT_DECODE
+    w, s = synth.weight(n, k, seed=n + k + 1)
+    x = synth.activations(m, k, seed=m + 12)
+    wd, sd, xd = w.cuda(), s.cuda(), x.cuda()
+    y = ops.block_fp8_gemm(xd, wd, sd)
+    yp = ops.block_fp8_gemm(xd, ops.pack_weight(wd), sd)
+    assert torch.equal(y.view(torch.int16), yp.view(torch.int16))
+    rows = torch.arange(0, m, 3)
+    assert_parity(y[rows.cuda()].cpu(), block_fp8.reference(x[rows], w, s), f"{m}x{n}x{k}")

@@ -60,6 +60,32 @@ def test_routing_ties_and_skew():
     check_routing(lg, 2)
 
 
+def test_routing_oversized_row_buffer_fully_defined():
+    # row_token larger than gk_fp8_moe_rows_max: every entry past the layout reads -1
+    import ctypes
+    from gaudi_kernels import _native as nat
+    t, e, k = 300, 8, 2
+    logits = torch.randn(t, e, generator=torch.Generator().manual_seed(11))
+    rows = ops.moe_rows_max(t, e, k)
+    extra = 3000
+    dev = torch.device("cuda")
+    lg = logits.to(dev)
+    ids = torch.empty((t, k), dtype=torch.int32, device=dev)
+    wts = torch.empty((t, k), dtype=torch.float32, device=dev)
+    row_of = torch.empty((t, k), dtype=torch.int32, device=dev)
+    row_token = torch.full((rows + extra,), 0x5A5A5A5A, dtype=torch.int32, device=dev)
+    off = torch.empty(e + 1, dtype=torch.int32, device=dev)
+    p = lambda x: ctypes.c_void_p(x.data_ptr())
+    st = nat.load().gk_fp8_moe_route(p(lg), t, e, e, k, p(ids), p(wts), p(row_of), p(row_token), rows + extra,
+                                     p(off), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == nat.GK_SUCCESS
+    ids_ref, _ = moe.route(logits.numpy(), k)
+    rt_ref, _, _, _, _ = moe.layout(ids_ref, e, 256)
+    rt = row_token.cpu().numpy()
+    assert np.array_equal(rt[: len(rt_ref)], rt_ref)
+    assert np.all(rt[len(rt_ref):] == -1)
+
+
 def problem(t, h, inter, e, seed, device="cpu"):
     x = synth.activations(t, h, seed)
     gen = torch.Generator().manual_seed(seed + 1)
