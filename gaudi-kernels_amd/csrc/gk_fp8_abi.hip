@@ -391,6 +391,54 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
   return run_gemm(p, q, sa, m, k, w, n, scales, bias, y, ldy, flags, packed, s);
 }
 
+// ---- allocation-free GEMM entry -----------------------------------------------------------
+// The quantized-activation scratch of gk_fp8_block_gemm_bf16_noalloc lives in
+// this file-scope device array (one copy per GPU, held until the process
+// ends).  Host code never passes `scratch` itself to a kernel: its device
+// address, per device, comes from hipGetSymbolAddress on the first call on
+// that device and is what the kernels receive.
+namespace {
+
+static_assert(GK_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch is used as a 256-byte aligned workspace");
+static __device__ __align__(256) uint8_t scratch[GK_NOALLOC_SCRATCH_BYTES];
+
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of `scratch` on the current device (nullptr on failure).
+void* scratch_address(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+  });
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+gk_status gk_fp8_block_gemm_bf16_noalloc(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
+                                         const float* scales, int64_t scale_rows, int64_t scale_cols,
+                                         const float* bias, void* y, int64_t ldy, uint32_t flags, void* stream) {
+  if (!x) return GK_INVALID_ARGUMENT;
+  Plan p;
+  gk_status st = make_plan(m, n, k, flags, w, &p);
+  if (st != GK_SUCCESS) return st;
+  if (p.q_bytes + p.sa_bytes > size_t{GK_NOALLOC_SCRATCH_BYTES}) return GK_INSUFFICIENT_BUFFER;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return GK_DEVICE_ERROR;
+  void* ws = scratch_address(dev);
+  if (!ws) return GK_DEVICE_ERROR;
+  // The quantizer rewrites every byte of the scratch the GEMM reads (padding rows included), so nothing left
+  // by an earlier call is read.
+  return gk_fp8_block_gemm_bf16(x, m, k, ldx, w, n, scales, scale_rows, scale_cols, bias, y, ldy, flags, ws,
+                                GK_NOALLOC_SCRATCH_BYTES, stream);
+}
+
 gk_status gk_fp8_block_gemm_q_bf16(const void* q, const float* sa, int64_t m, int64_t m_pad, int64_t k,
                                    const void* w, int64_t n, const float* scales, int64_t scale_rows,
                                    int64_t scale_cols, const float* bias, void* y, int64_t ldy, uint32_t flags,

@@ -73,6 +73,8 @@ SIGNATURES = {
                                         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_size)]),
     "gk_fp8_block_gemm_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _c_i64, _c_i64, _fp,
                                         _c_vp, _c_i64, _c_u32, _c_vp, _c_size, _c_vp]),
+    "gk_fp8_block_gemm_bf16_noalloc": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _c_i64, _c_i64,
+                                                _fp, _c_vp, _c_i64, _c_u32, _c_vp]),
     "gk_fp8_block_gemm_q_bf16": (_c_int, [_c_vp, _fp, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp, _c_i64, _c_i64,
                                           _fp, _c_vp, _c_i64, _c_u32, _c_vp]),
     "gk_fp8_block_gemm_kslice_f32": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _fp,

@@ -165,6 +165,25 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
                                  void* y, int64_t ldy, uint32_t flags, void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* Scratch of gk_fp8_block_gemm_bf16_noalloc (bytes, per GPU): enough for
+ * the quantized activations of config 4's M = 4096, K = 7168. */
+#define GK_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* gk_fp8_block_gemm_bf16 without a workspace argument and without any
+ * allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The quantized activations go to
+ * a fixed scratch array of GK_NOALLOC_SCRATCH_BYTES in the library's code
+ * object, one per GPU, held until the process ends; plans needing more
+ * (gk_fp8_block_gemm_plan's workspace_bytes) -> GK_INSUFFICIENT_BUFFER before
+ * any device work.  Results are those of gk_fp8_block_gemm_bf16 bit for bit.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap in time
+ * on one GPU (different streams, or several host threads) race and must be
+ * ordered by the caller. */
+gk_status gk_fp8_block_gemm_bf16_noalloc(const void* x, int64_t m, int64_t k, int64_t ldx, const void* w, int64_t n,
+                                         const float* scales, int64_t scale_rows, int64_t scale_cols,
+                                         const float* bias, void* y, int64_t ldy, uint32_t flags, void* stream);
+
 /* The same GEMM on activations already quantized by gk_fp8_act_quant_bf16
  * (q [G][m_pad][128], sa [G][m_pad]); m_pad must equal the plan's m_pad for
  * these flags.  GK_FLAG_DECODE_LAYOUT: q is in the decode fragment layout
