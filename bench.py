@@ -1,6 +1,8 @@
 """Benchmark of the MI355X block-FP8 W8A8 GEMM (BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode|qkv|side|prefill|mlp|moe]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only qkv|side|prefill|mlp|moe|ceiling]
+    python bench.py --profile config2|prefill|mlp|moe [--reps R]    # eager launches only, for rocprofv3 runs
+    python bench.py --rocprof-summary DIR                          # tables of a rocprofv3 csv output
 
 Workload (one "step"): BASELINE.json configs[1] decode sweep -- one block-FP8
 GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
@@ -19,8 +21,11 @@ in the same JSON line: the prefill config (M=4096, N=K=7168; TFLOP/s against
 the dense FP8 MFMA peak), the MLP-pair decode config, the MoE layer (512
 tokens, 8 experts, top-2, H=4096, I=14336), the per-M sweep, the
 roofline of the dominant kernel (the decode GEMM with the quantizer fused,
-averaged over the step's five launches; HIP events on its stream) and
-the CPU oracle baseline timed on this host.
+averaged over the step's five launches; HIP events on its stream), the
+prefill kernel's roofline against the dense FP8 MFMA peak (roofline_prefill),
+the streaming-read ceiling of this GPU at the decode footprints
+(stream_ceiling, libgk_probe.so) and the CPU oracle baseline timed on this
+host (config 2 M=16 as cpu_baseline; configs 3, 4 and 5 beside it).
 """
 
 import argparse
@@ -43,6 +48,9 @@ MALL_ROTATE_BYTES = 512 << 20
 # (NW=8, R=2, U=4, bf16 activations read directly, WPACK, one token tile) -- each op of the step is one
 # launch of it.
 DECODE_KERNEL = "gk::gemm_decode_kernel<8,2,4,false,false,false,true,true,1>"
+# The prefill roofline kernel: the 256 x 256 LDS-tiled MFMA kernel on packed weights (config 4).
+PREFILL_KERNEL = "gk::gemm_prefill256_kernel<false,false,false,true>"
+SIMD_NUM = 1024  # 256 CUs x 4 SIMDs (MI355X)
 
 
 def gemm_bytes(m, n, k, bias=False):
@@ -117,6 +125,19 @@ def time_loop(fn, iters, warmup):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "block_fp8_gemm_bench.md")
+PROFILE_DIR = os.path.join(ROOT, "profiles")
+
+
+def profile_lines():
+    """Lines of every committed rocprofv3 summary under profiles/ (traffic: and mfma: lines are read from them)."""
+    import glob
+    lines = []
+    for path in sorted(glob.glob(os.path.join(PROFILE_DIR, "*.md"))):
+        try:
+            lines += open(path).read().splitlines()
+        except OSError:
+            pass
+    return lines
 
 
 def measured_traffic(kernel_prefix, workload):
@@ -124,14 +145,22 @@ def measured_traffic(kernel_prefix, workload):
     committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration),
     or None if not recorded."""
     import re
-    try:
-        text = open(TRAFFIC_PROFILE).read()
-    except OSError:
-        return None
-    for line in text.splitlines():
+    for line in profile_lines():
         m = re.match(r"traffic: kernel=(\S+) workload=(\S+) .* bytes=(\d+)", line)
         if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload:
             return int(m.group(3))
+    return None
+
+
+def measured_mfma(kernel_prefix, workload):
+    """(MFMA busy fraction, F8 MFMA FLOPs per launch, GRBM_GUI_ACTIVE cycles) of the kernel on `workload` from the
+    committed rocprofv3 --pmc summary, or None if not recorded."""
+    import re
+    for line in profile_lines():
+        m = re.match(r"mfma: kernel=(\S+) workload=(\S+) .*busy_frac=([0-9.]+) .*f8_flops=([0-9.e+]+) .*gui_cycles=([0-9.]+)",
+                     line)
+        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload:
+            return float(m.group(3)), float(m.group(4)), float(m.group(5))
     return None
 
 
@@ -193,15 +222,213 @@ def rocprof_summary(directory):
         print(f"copy calibration: FETCH_SIZE {copy['FETCH_SIZE']:.1f} KiB and WRITE_SIZE {copy['WRITE_SIZE']:.1f} KiB "
               f"for {copy_bytes} bytes each way: scales {fs:.4f} / {ws:.4f}\n")
         for (name, grid, ctr), v in sorted(counters.items()):
-            if ctr != "FETCH_SIZE" or not name.replace("void ", "").startswith("gk::gemm_decode_kernel"):
+            short = name.replace("void ", "")
+            if ctr != "FETCH_SIZE" or not short.startswith("gk::gemm_"):
                 continue
             wv = counters.get((name, grid, "WRITE_SIZE"))
             if not wv:
                 continue
             f_kib, w_kib = med(v), med(wv)
             total = int(round(f_kib * 1024 * fs + w_kib * 1024 * ws))
-            print(f"traffic: kernel={name.replace('void ', '').replace(' ', '')} workload=config2 grid={grid} fetch_kib={f_kib:.1f} "
-                  f"write_kib={w_kib:.1f} fetch_scale={fs:.4f} write_scale={ws:.4f} bytes={total}\n")
+            print(f"traffic: kernel={short.replace(' ', '')} workload={WORKLOAD_BY_GRID.get(grid, 'grid' + grid)} "
+                  f"grid={grid} fetch_kib={f_kib:.1f} write_kib={w_kib:.1f} fetch_scale={fs:.4f} write_scale={ws:.4f} "
+                  f"bytes={total}\n")
+    # Matrix-core evidence: MfmaUtil (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, percent),
+    # SQ_INSTS_VALU_MFMA_MOPS_F8 (FLOPs / 512) and GRBM_GUI_ACTIVE per dispatch shape.
+    for (name, grid, ctr), v in sorted(counters.items()):
+        short = name.replace("void ", "")
+        if ctr != "MfmaUtil" or not short.startswith("gk::gemm_"):
+            continue
+        mops = counters.get((name, grid, "SQ_INSTS_VALU_MFMA_MOPS_F8"))
+        gui = counters.get((name, grid, "GRBM_GUI_ACTIVE"))
+        if not mops or not gui:
+            continue
+        print(f"mfma: kernel={short.replace(' ', '')} workload={WORKLOAD_BY_GRID.get(grid, 'grid' + grid)} grid={grid} "
+              f"busy_frac={med(v) / 100:.4f} f8_flops={med(mops) * 512:.6e} gui_cycles={med(gui):.0f}\n")
+
+
+# Dispatch grids (threads) of the bench workloads' GEMM kernels -> workload names in profile summaries.
+WORKLOAD_BY_GRID = {"98304": "config2", "114688": "config3_gate_up", "131072": "config3_down",
+                    "229376": "config4", "688128": "config5_gate_up", "196608": "config5_down"}
+
+
+def copy_calibration():
+    """Plain device-to-device copy of 256 MiB: the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters of
+    `rocprofv3 --pmc` runs of this script (the GEMM counters are scaled by what they read here)."""
+    copy_bytes = 256 << 20
+    csrc = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
+    cdst = torch.empty_like(csrc)
+    for _ in range(3):
+        cdst.copy_(csrc)
+    torch.cuda.synchronize()
+
+
+def run_profile(workload, reps):
+    """Eager launches of one workload for rocprofv3 (kernel trace or counters): the same inputs and ops as the
+    timed measurements, no graphs, no timing."""
+    from gaudi_kernels import ops
+    from oracle import synth
+
+    ops.require_device()
+    copy_calibration()
+    log(f"[profile] {workload}, {reps} reps")
+    if workload == "config2":
+        n, k = 6144, 4096
+        w, s = synth.weight(n, k, seed=2000)
+        p, sd = ops.pack_weight(w.cuda()), s.cuda()
+        for m in (1, 2, 4, 8, 16):
+            x = synth.activations(m, k, seed=2001 + m).cuda()
+            for _ in range(reps):
+                ops.block_fp8_gemm(x, p, sd)
+    elif workload == "prefill":
+        m, n, k = 4096, 7168, 7168
+        w, s = synth.weight(n, k, seed=4000)
+        x = synth.activations(m, k, seed=4001).cuda()
+        p, sd = ops.pack_weight(w.cuda()), s.cuda()
+        o = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        for _ in range(reps):
+            ops.block_fp8_gemm(x, p, sd, out=o)
+    elif workload == "mlp":
+        m = 16
+        for (n, k, seed) in ((28672, 4096, 3000), (4096, 14336, 3100)):
+            w, s = synth.weight(n, k, seed=seed)
+            x = synth.activations(m, k, seed=seed + 1).cuda()
+            p, sd = ops.pack_weight(w.cuda()), s.cuda()
+            for _ in range(reps):
+                ops.block_fp8_gemm(x, p, sd)
+    elif workload == "moe":
+        x5, lg5, wg, sg, wdn, sdn = moe_inputs()
+        pg, pdn = ops.pack_experts(wg), ops.pack_experts(wdn)
+        for _ in range(reps):
+            ops.moe_block_fp8(x5, lg5, pg, sg, pdn, sdn, top_k=2)
+    torch.cuda.synchronize()
+    log("[profile] done")
+
+
+def moe_inputs(device="cuda"):
+    """Config 5 (512 tokens, 8 experts, top-2, H=4096, I=14336) on `device`."""
+    from oracle import synth
+    t5, h5, i5, e5 = 512, 4096, 14336, 8
+    wg, sg, wdn, sdn = [], [], [], []
+    for i in range(e5):
+        a, b = synth.weight(2 * i5, h5, seed=5010 + i, device=device)
+        c, d = synth.weight(h5, i5, seed=6010 + i, device=device)
+        wg.append(a); sg.append(b); wdn.append(c); sdn.append(d)
+    x5 = synth.activations(t5, h5, seed=5001).to(device)
+    lg5 = torch.randn(t5, e5, generator=torch.Generator().manual_seed(5002)).to(device)
+    return x5, lg5, torch.stack(wg), torch.stack(sg), torch.stack(wdn), torch.stack(sdn)
+
+
+def stream_ceiling():
+    """Best streaming-read rate (GB/s) of a plain read kernel (libgk_probe.so) at the decode footprints: config 2's
+    weights (25.17 MB) and config 3's gate_up weights (117.44 MB), buffers rotated over >= 512 MB like the GEMMs,
+    workgroup counts 256..4096."""
+    import ctypes
+    path = os.path.join(ROOT, "gaudi-kernels_amd", "python", "gaudi_kernels", "libgk_probe.so")
+    lib = ctypes.CDLL(path)
+    lib.gk_probe_stream_read.restype = ctypes.c_int
+    lib.gk_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                         ctypes.c_void_p]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    out = {}
+    for label, nbytes in (("config2_25MB", 6144 * 4096), ("config3_gate_up_117MB", 28672 * 4096)):
+        copies = max(2, -(-MALL_ROTATE_BYTES // nbytes))
+        bufs = [torch.full((nbytes,), i + 1, dtype=torch.uint8, device="cuda") for i in range(copies)]
+        best = None
+        for wgs in (256, 512, 1024, 2048, 4096):
+            state = {"i": 0}
+
+            def read():
+                b = bufs[state["i"]]
+                state["i"] = (state["i"] + 1) % copies
+                st = lib.gk_probe_stream_read(ctypes.c_void_p(b.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()),
+                                              wgs, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                assert st == 0, st
+
+            t = time_loop(read, 4 * copies, 3)
+            gbs = nbytes / (t * 1e-3) / 1e9
+            if best is None or gbs > best[0]:
+                best = (gbs, wgs, t * 1e3)
+        out[label] = {"bytes": nbytes, "GBps": round(best[0], 1), "hbm_frac": round(best[0] / PEAK_HBM_GBS, 4),
+                      "us": round(best[2], 2), "workgroups": best[1]}
+        del bufs
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baselines(w2, s2):
+    """The oracle (oracle/block_fp8.reference, oracle/moe.moe_reference: block_fp8_oracle.py:11-46 batched over
+    rows) on this host's cores.  Returns (headline config 2 M=16 entry, per-config entries)."""
+    from oracle import block_fp8, moe, synth
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    model = cpu_model()
+
+    def median_time(fn, min_runs=3, budget_s=10.0):
+        fn()  # warm-up
+        times = []
+        t_budget = time.perf_counter()
+        while len(times) < min_runs or (time.perf_counter() - t_budget < budget_s and len(times) < 10):
+            t1 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t1)
+            if len(times) >= 1 and time.perf_counter() - t_budget > 3 * budget_s:
+                break
+        return sorted(times)[len(times) // 2], len(times)
+
+    base = {"cores": cores, "cpu_model": model, "kind": "port"}
+    # config 2, M = 16 (the headline unit: GB/s)
+    n, k, m = 6144, 4096, 16
+    xc = synth.activations(m, k, seed=2001 + m)
+    t2, r2 = median_time(lambda: block_fp8.reference(xc, w2, s2, row_chunk=16))
+    headline = {"value": round(gemm_bytes(m, n, k) / t2 / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                "sample": f"oracle/block_fp8.reference, config2 M=16 N=6144 K=4096 in full, median of {r2} runs "
+                          f"({t2 * 1e3:.0f} ms each), torch threads={cores}, cpu {model}"}
+    per = {"config2_m16": {**base, "s": round(t2, 4), "GBps": headline["value"], "runs": r2, "sample": "full"}}
+    # config 3: the MLP pair at M = 16, in full
+    tot_t, tot_b = 0.0, 0
+    for (nn, kk, seed) in ((28672, 4096, 3000), (4096, 14336, 3100)):
+        w3, s3 = synth.weight(nn, kk, seed=seed)
+        x3 = synth.activations(16, kk, seed=seed + 1)
+        t3, _ = median_time(lambda: block_fp8.reference(x3, w3, s3, row_chunk=16), min_runs=1, budget_s=3.0)
+        tot_t += t3
+        tot_b += gemm_bytes(16, nn, kk)
+        del w3, s3
+    per["config3_mlp_pair_m16"] = {**base, "s": round(tot_t, 4), "GBps": round(tot_b / tot_t / 1e9, 3),
+                                   "sample": "full (gate_up N=28672 K=4096 + down N=4096 K=14336, M=16)"}
+    # config 4: 64-row chunks, two timed and extrapolated to the 64 chunks of M = 4096
+    m4, n4, k4 = 4096, 7168, 7168
+    w4, s4 = synth.weight(n4, k4, seed=4000)
+    x4 = synth.activations(128, k4, seed=4001)
+    block_fp8.reference(x4[:64], w4, s4, row_chunk=64)  # warm-up
+    t1 = time.perf_counter()
+    block_fp8.reference(x4, w4, s4, row_chunk=64)
+    tc = (time.perf_counter() - t1) / 2
+    t4 = tc * (m4 // 64)
+    per["config4_prefill"] = {**base, "s": round(t4, 2), "TFLOPs": round(gemm_flops(m4, n4, k4) / t4 / 1e12, 5),
+                              "sample": f"extrapolated: 2 of 64 row chunks of 64 timed ({tc:.2f} s per chunk) x 64",
+                              "extrapolated": True}
+    del w4, s4
+    # config 5: the MoE layer in full
+    x5, lg5, wg, sg, wdn, sdn = moe_inputs(device="cpu")
+    t1 = time.perf_counter()
+    moe.moe_reference(x5, lg5, wg, sg, wdn, sdn, top_k=2)
+    t5 = time.perf_counter() - t1
+    w_bytes = wg.numel() + wdn.numel() + 4 * (sg.numel() + sdn.numel())
+    f5 = 2 * 512 * 2 * (2 * 14336 * 4096 + 4096 * 14336)
+    per["config5_moe"] = {**base, "s": round(t5, 2), "GBps": round(w_bytes / t5 / 1e9, 3),
+                          "TFLOPs": round(f5 / t5 / 1e12, 5), "sample": "full (one run), oracle/moe.moe_reference"}
+    return headline, per
 
 
 def main():
@@ -210,9 +437,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["decode", "qkv", "side", "prefill", "mlp", "moe"], default=None)
+    ap.add_argument("--only", choices=["decode", "qkv", "side", "prefill", "mlp", "moe", "ceiling"], default=None)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
                     help="print per-kernel, per-grid tables of a rocprofv3 csv output directory and exit")
+    ap.add_argument("--profile", choices=["config2", "prefill", "mlp", "moe"], default=None,
+                    help="run one workload's ops eagerly (for rocprofv3) and exit")
+    ap.add_argument("--reps", type=int, default=5)
     args = ap.parse_args()
     if args.rocprof_summary:
         rocprof_summary(args.rocprof_summary)
@@ -221,6 +451,10 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (under tensor parallelism each GPU "
               "runs this GEMM on its own shard of the weights); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.profile:
+        run_profile(args.profile, args.reps)
+        return
 
     from gaudi_kernels import ops
     from oracle import synth
@@ -294,16 +528,7 @@ def main():
     del rot, rot_row
     torch.cuda.empty_cache()
 
-    # Plain device-to-device copy of a known size: the calibration kernel for
-    # the FETCH_SIZE / WRITE_SIZE counters read by `rocprofv3 --pmc` runs of
-    # this script (the counters of the GEMM are scaled by what they read here).
-    copy_bytes = 256 << 20
-    csrc = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
-    cdst = torch.empty_like(csrc)
-    for _ in range(3):
-        cdst.copy_(csrc)
-    torch.cuda.synchronize()
-    del csrc, cdst
+    copy_calibration()
 
     # Average launch of the step's kernel: algorithmic bytes per launch (the
     # mean over M = 1..16 of N*K + 4*(N/128)*(K/128) + 2*M*K + 2*M*N) over the
@@ -314,12 +539,19 @@ def main():
     result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(achieved / PEAK_HBM_GBS, 4),
                           "traffic": measured_traffic(DECODE_KERNEL, "config2"),
-                          "traffic_source": "profiles/block_fp8_gemm_bench.md (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
+                          "traffic_source": "profiles/ (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
                           "kernel": f"{DECODE_KERNEL} (quantizer fused; M=1,2,4,8,16, N=6144, K=4096, packed weights)",
                           "bytes_per_launch": int(avg_bytes), "avg_launch_us": round(avg_us, 3),
                           "m16": {"achieved": round(gemm_bytes(16, n, k) / (launch_us[-1] * 1e-6) / 1e9, 1),
                                   "launch_us": round(launch_us[-1], 3)}}
     result["decode_sweep"] = per_m
+
+    # ---- the streaming-read ceiling at the decode footprints --------------------------------------
+    if args.only in (None, "ceiling"):
+        ceil = stream_ceiling()
+        ceil["decode_roofline_frac_of_ceiling"] = round(result["roofline"]["achieved"] / ceil["config2_25MB"]["GBps"], 4)
+        result["stream_ceiling"] = ceil
+        log(f"[bench] stream ceiling: {ceil}")
 
     # ---- config 2 as a layer step: fused add + RMSNorm feeding the QKV GEMM --------------------------
     # (a) one norm kernel that also writes the 1x128 codes in the decode layout, then the GEMM on them;
@@ -446,34 +678,46 @@ def main():
         m, nn, kk = 4096, 7168, 7168
         w4, s4 = synth.weight(nn, kk, seed=4000)
         x4 = synth.activations(m, kk, seed=4001).cuda()
-        w4d, s4d = w4.cuda(), s4.cuda()
-        p4 = ops.pack_weight(w4d)
+        # weight copies rotated (>= 512 MB with the codes and the output) so that the MALL does not hold them
+        r4 = Rotation(w4, s4, min_bytes=384 << 20, packed=True)
+        r4r = Rotation(w4, s4, min_bytes=384 << 20)
         o4 = torch.empty((m, nn), dtype=torch.bfloat16, device="cuda")
         ws4 = ops.make_workspace(m, nn, kk)
-        ms4 = time_loop(lambda: ops.block_fp8_gemm(x4, p4, s4d, out=o4, workspace=ws4), 20, 3)
+        ms4 = time_loop(lambda: ops.block_fp8_gemm(x4, *r4.next(), out=o4, workspace=ws4), 2 * len(r4.items), 3)
         _, m_pad, _ = ops.plan(m, nn, kk)
         q4, sa4 = ops.act_quant(x4, m_pad=m_pad)
-        ms4k = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, p4, s4d, out=o4), 20, 3)
-        ms4r = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, w4d, s4d, out=o4), 20, 3)
+        ms4k = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, *r4.next(), out=o4), 2 * len(r4.items), 3)
+        ms4r = time_loop(lambda: ops.block_fp8_gemm_q(q4, sa4, m, *r4r.next(), out=o4), 2 * len(r4r.items), 3)
+        del r4, r4r
+        torch.cuda.empty_cache()
         f = gemm_flops(m, nn, kk)
         result["prefill_m4096"] = {"op_us": round(ms4 * 1e3, 1), "gemm_kernel_us": round(ms4k * 1e3, 1),
                                    "op_TFLOPs": round(f / (ms4 * 1e-3) / 1e12, 1),
+                                   "op_mfma_frac": round(f / (ms4 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
                                    "gemm_kernel_TFLOPs": round(f / (ms4k * 1e-3) / 1e12, 1),
                                    "gemm_kernel_mfma_frac": round(f / (ms4k * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
-                                   "gemm_kernel_rowmajor_us": round(ms4r * 1e3, 1)}
+                                   "gemm_kernel_rowmajor_us": round(ms4r * 1e3, 1),
+                                   "weights": "packed, rotated copies (not MALL-resident)"}
+        # The prefill kernel's roofline: FLOPs of one launch over its average launch duration (graph replay of
+        # back-to-back launches on the replay stream, HIP events), against the dense FP8 MFMA peak.
+        achieved = f / (ms4k * 1e-3) / 1e12
+        counters = measured_mfma(PREFILL_KERNEL, "config4")
+        result["roofline_prefill"] = {
+            "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": measured_traffic(PREFILL_KERNEL, "config4"),
+            "kernel": f"{PREFILL_KERNEL} (config 4: M=4096, N=K=7168, packed weights, activations quantized "
+                      "beforehand)",
+            "flops_per_launch": f, "avg_launch_us": round(ms4k * 1e3, 2), "op_frac": round(f / (ms4 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "counters": None if counters is None else {
+                "mfma_busy_frac": counters[0], "f8_mfma_flops": counters[1], "gui_active_cycles": counters[2],
+                "source": "profiles/prefill_moe_gemm_counters.md (rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_F8 "
+                          "GRBM_GUI_ACTIVE)"}}
         log(f"[bench] prefill: {result['prefill_m4096']}")
 
     # ---- config 5: MoE layer ----------------------------------------------------------------------
     if args.only in (None, "moe"):
         t5, h5, i5, e5, k5 = 512, 4096, 14336, 8, 2
-        wg, sg, wdn, sdn = [], [], [], []
-        for i in range(e5):
-            a, b = synth.weight(2 * i5, h5, seed=5010 + i, device="cuda")
-            c, d = synth.weight(h5, i5, seed=6010 + i, device="cuda")
-            wg.append(a); sg.append(b); wdn.append(c); sdn.append(d)
-        wg, sg, wdn, sdn = torch.stack(wg), torch.stack(sg), torch.stack(wdn), torch.stack(sdn)
-        x5 = synth.activations(t5, h5, seed=5001).cuda()
-        lg5 = torch.randn(t5, e5, generator=torch.Generator().manual_seed(5002)).cuda()
+        x5, lg5, wg, sg, wdn, sdn = moe_inputs()
         o5 = torch.empty((t5, h5), dtype=torch.bfloat16, device="cuda")
         ws5 = torch.empty(ops.moe_workspace_bytes(t5, h5, i5, e5, k5), dtype=torch.uint8, device="cuda")
         ms5r = time_loop(lambda: ops.moe_block_fp8(x5, lg5, wg, sg, wdn, sdn, top_k=k5, out=o5, workspace=ws5),
@@ -504,23 +748,9 @@ def main():
     # ---- CPU baseline: the oracle on this host ----------------------------------------------------
     cpu = None
     if not args.no_cpu:
-        from oracle import block_fp8
-        cores = os.cpu_count() or 1
-        torch.set_num_threads(cores)
-        m = 16
-        xc = synth.activations(m, k, seed=2001 + m)
-        block_fp8.reference(xc[:1], w, s)  # warm-up
-        times = []
-        t_budget = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - t_budget < 10 and len(times) < 10):
-            t1 = time.perf_counter()
-            block_fp8.reference(xc, w, s, row_chunk=16)
-            times.append(time.perf_counter() - t1)
-        tmed = sorted(times)[len(times) // 2]
-        cpu = {"value": round(gemm_bytes(m, n, k) / tmed / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-               "sample": f"oracle/block_fp8.reference, config2 M=16 N=6144 K=4096, median of {len(times)} runs "
-                         f"({tmed * 1e3:.0f} ms each), torch threads={cores}"}
-        log(f"[bench] cpu baseline: {cpu}")
+        cpu, per_cfg = cpu_baselines(w, s)
+        result["cpu_baseline_configs"] = per_cfg
+        log(f"[bench] cpu baseline: {cpu} {per_cfg}")
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

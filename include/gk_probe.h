@@ -1,0 +1,25 @@
+/* gk_probe.h -- measurement probe used by bench.py (libgk_probe.so).  Not part
+ * of the block-FP8 library and not a reference interface: it has no
+ * counterpart in the reference, which publishes no performance figures.
+ *
+ * gk_probe_stream_read reads `bytes` of device memory at `src` (16-byte
+ * aligned, a multiple of 16) with `workgroups` workgroups of 256 lanes and
+ * 16-byte non-temporal loads, and writes nothing to `sink` (a device word)
+ * unless the data folds to a sentinel.  Asynchronous on `stream` (hipStream_t
+ * as void*).  Returns 0, 1 for bad arguments, 2 for a launch error. */
+#ifndef GK_PROBE_H
+#define GK_PROBE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int gk_probe_stream_read(const void* src, size_t bytes, void* sink, int workgroups, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GK_PROBE_H */

@@ -239,3 +239,20 @@ def test_partial_finish_rejections_before_device_use():
     assert f(fake, 2, 16, 16, None, fake, 8, None) == nat.GK_INCOMPATIBLE_OUTPUT_SIZE
     assert f(fake, 2, 16, 16, ctypes.c_void_p((1 << 20) + 2), fake, 16, None) == nat.GK_INCOMPATIBLE_DATA_TYPE
     assert f(None, 2, 16, 16, None, fake, 16, None) == nat.GK_INVALID_ARGUMENT
+
+
+def test_probe_library_exports_match_its_header():
+    """libgk_probe.so (bench.py's streaming-read ceiling) exports exactly what include/gk_probe.h declares."""
+    probe = os.path.join(os.path.dirname(nat.lib_path()), "libgk_probe.so")
+    if not os.path.exists(probe):
+        pytest.skip("libgk_probe.so not built")
+    text = open(os.path.join(ROOT, "include", "gk_probe.h")).read()
+    want = sorted(set(re.findall(r"^\s*int\s+(gk_\w+)\s*\(", text, re.MULTILINE)))
+    out = subprocess.run(["nm", "-D", "--defined-only", probe], check=True, capture_output=True, text=True).stdout
+    have = sorted({l.split()[-1] for l in out.splitlines() if " T " in l and l.split()[-1].startswith("gk_")})
+    assert have == want == ["gk_probe_stream_read"]
+    lib = ctypes.CDLL(probe)
+    lib.gk_probe_stream_read.restype = ctypes.c_int
+    lib.gk_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                         ctypes.c_void_p]
+    assert lib.gk_probe_stream_read(ctypes.c_void_p(1 << 20), 17, ctypes.c_void_p(1 << 20), 256, None) == 1

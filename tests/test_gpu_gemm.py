@@ -24,6 +24,7 @@ SENTINEL = 0x7E7E  # bf16 bit pattern never produced by these inputs
 
 def assert_parity(y, ref, tag=""):
     max_rel, mean_rel = block_fp8.parity(y, ref)
+    print(f"parity {tag}: max_rel {max_rel:.3e} mean_rel {mean_rel:.3e}", flush=True)
     assert max_rel <= block_fp8.MAX_REL_TOL and mean_rel <= block_fp8.MEAN_REL_TOL, (tag, max_rel, mean_rel)
     return max_rel, mean_rel
 
@@ -60,6 +61,54 @@ def test_config2_qkv_decode(m):
     ref = block_fp8.reference(x, w, s)
     for variant in (None, "prefill"):
         assert_parity(run(x, w, s, variant=variant), ref, f"M={m}/{variant}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+def test_config2_packed_fused_quantizer_against_oracle(m):
+    """The benchmarked path itself -- packed weights, the 1x128 quantizer fused into the decode kernel
+    (one launch, gemm_decode_kernel<8,2,4,...,WPACK,XQ,1>) -- against the oracle, not only through
+    bit-identity with the unfused and row-major forms."""
+    n, k = 6144, 4096
+    w, s = synth.weight(n, k, seed=2000)
+    x = synth.activations(m, k, seed=2001 + m)
+    p = ops.pack_weight(w.cuda())
+    assert ops.plan(m, n, k, 32, p.data)[0] == 1  # GK_VARIANT_DECODE on GK_FLAG_WEIGHT_PACKED weights
+    y = ops.block_fp8_gemm(x.cuda(), p, s.cuda()).cpu()
+    assert_parity(y, block_fp8.reference(x, w, s), f"packed fused M={m}")
+
+
+def test_config3_packed_against_oracle():
+    m = 16
+    for (n, k, seed) in ((28672, 4096, 3000), (4096, 14336, 3100)):
+        w, s = synth.weight(n, k, seed=seed)
+        x = synth.activations(m, k, seed=seed + 1)
+        y = ops.block_fp8_gemm(x.cuda(), ops.pack_weight(w.cuda()), s.cuda()).cpu()
+        assert_parity(y, block_fp8.reference(x, w, s, row_chunk=16), f"packed N={n} K={k}")
+
+
+@pytest.mark.parametrize("native_half", [False, True])
+def test_config1_as_specified(native_half):
+    """BASELINE.json config 1 end to end on the GPU: W [256, 256] N(0, 0.02) seed 0 quantized per 128x128 block
+    with scale = blockmax / 240 (Gaudi2 half range), codec forward to half range and inverse back to OCP on the
+    GPU, then the GEMM on the round-tripped codes against the oracle on the same codes."""
+    from oracle import fp8_codec
+    x, w, s = synth.config1()
+    assert int(w.view(torch.uint8).bitwise_and(0x7F).max()) <= 0x77         # D = 240 keeps codes <= 0x77
+    half, s2, rounded = ops.codec_ocp_to_half(w.cuda(), s.cuda())
+    want_half, want_s2, want_rounded = fp8_codec.reencode_e4m3fn_half(w.view(torch.uint8).numpy(), s.numpy())
+    assert rounded == want_rounded and torch.equal(half.cpu(), torch.from_numpy(want_half))
+    assert torch.equal(s2.cpu(), torch.from_numpy(want_s2))
+    back, s_back = ops.codec_half_to_ocp(half, s2)
+    want_back, want_s_back = fp8_codec.decode_half_to_ocp(want_half, want_s2)
+    assert torch.equal(back.cpu(), torch.from_numpy(want_back)) and torch.equal(s_back.cpu(), torch.from_numpy(want_s_back))
+    w_rt = back.cpu().view(torch.float8_e4m3fn)
+    # the round trip changes only the codes the forward codec rounds
+    changed = int((w_rt.view(torch.uint8) != w.view(torch.uint8)).sum())
+    assert changed <= rounded
+    for variant in (None, "decode", "prefill", "generic"):
+        y = ops.block_fp8_gemm(x.cuda(), back.view(torch.float8_e4m3fn), s_back, native_half=native_half,
+                               variant=variant).cpu()
+        assert_parity(y, block_fp8.reference(x, w_rt, s_back.cpu(), native_half=native_half), f"config1/{variant}")
 
 
 def test_config3_mlp_pair_decode():

@@ -5,8 +5,8 @@ row_token, row_of and offsets must be bit-exact; the two softmax weights are
 fp32 and within a few ulp (the device exp).  The layer output must meet the GEMM
 gate (max|y - ref| <= 1e-2 max|ref|, sum|y - ref| / sum|ref| <= 2e-3) at
 small sizes in full and at BASELINE.json config 5 (512 tokens, 8 experts, top-2,
-H=4096, I=14336) stage by stage on sampled tokens and end to end within the
-chain bound below, plus the size-independent property that
+H=4096, I=14336) stage by stage on every routed row and end to end on all 512
+tokens within the chain bound below, plus the size-independent property that
 permuting tokens permutes the output bit-for-bit (every row's arithmetic is
 independent of the other rows).
 """
@@ -175,9 +175,9 @@ def regions(ws, t, h, inter, e, k):
     return {n: x.cpu() for n, x in v.items()}
 
 
-@pytest.mark.timeout(300)
+@pytest.mark.timeout(600)
 def test_moe_config5_stagewise_parity():
-    """Each stage of config 5 against the oracle, fed the device's own input to that stage.
+    """Each stage of config 5 against the oracle, fed the device's own input to that stage, on every routed row.
 
     gate_up and down: the GEMM gate per expert row set; SiLU-and-mul + quantization:
     codes equal to the oracle's on the device's gate_up output except where the
@@ -192,7 +192,7 @@ def test_moe_config5_stagewise_parity():
     row_of = r["row_of"].reshape(t, k).long()
     assert torch.equal(r["cnt"].long(), torch.bincount(ids.reshape(-1).long(), minlength=e))
     assert int(r["parts"]) == 2  # config 5: the down GEMM splits K
-    tokens = torch.randperm(t, generator=torch.Generator().manual_seed(2))[:12]
+    tokens = torch.arange(t)  # every routed row of every expert
     for x_e in range(e):
         pairs = [(int(tok), s) for tok in tokens for s in range(k) if int(ids[tok, s]) == x_e]
         if not pairs:
@@ -223,8 +223,8 @@ def test_moe_config5_stagewise_parity():
     assert torch.equal(y, acc.bfloat16())
 
 
-@pytest.mark.timeout(300)
-def test_moe_config5_sampled_parity_and_permutation():
+@pytest.mark.timeout(600)
+def test_moe_config5_end_to_end_parity_and_permutation():
     t, h, inter, e = 512, 4096, 14336, 8
     x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=5000, device="cuda")
     xg, lg = x.cuda(), logits.cuda()
@@ -236,9 +236,9 @@ def test_moe_config5_sampled_parity_and_permutation():
     ids, _ = moe.route(logits.numpy(), 2)
     counts = np.bincount(ids.reshape(-1), minlength=e)
     assert counts.min() > 0 and counts.max() != counts.min()        # uneven, every expert used
-    tokens = torch.randperm(t, generator=torch.Generator().manual_seed(2))[:12].tolist()
-    ref = moe.moe_reference(x, logits, wg.cpu(), sg.cpu(), wd.cpu(), sd.cpu(), top_k=2, tokens=tokens)
-    max_rel, mean_rel = block_fp8.parity(y.cpu()[tokens], ref)
+    ref = moe.moe_reference(x, logits, wg.cpu(), sg.cpu(), wd.cpu(), sd.cpu(), top_k=2)  # all 512 tokens
+    max_rel, mean_rel = block_fp8.parity(y.cpu(), ref)
+    print(f"config 5 end to end: max_rel {max_rel:.3e} mean_rel {mean_rel:.3e}", flush=True)
     assert max_rel <= CHAIN_MAX_REL and mean_rel <= CHAIN_MEAN_REL, (max_rel, mean_rel)
 
 
