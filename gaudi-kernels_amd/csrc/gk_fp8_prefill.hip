@@ -1,10 +1,10 @@
 // Large-M prefill block-FP8 GEMM for gfx950: 256 x 256 output tile per
-// workgroup, FP8 MFMA 32x32x64, per-128-K-group fp32 scale promotion.
+// workgroup, FP8 MFMA 16x16x128, per-128-K-group fp32 scale promotion.
 //
 // Same arithmetic as the other variants (block_fp8_oracle.py:38-46): each
-// 128-K group's exact fp8 x fp8 partial (two chained MFMAs over K = 64) is
-// multiplied by sa[m, g] * sw[n / 128, g] and accumulated in fp32; bias and
-// bf16 rounding happen in the epilogue.
+// 128-K group's fp8 x fp8 partial (one v_mfma_f32_16x16x128_f8f6f4 per 16 x 16
+// block) is multiplied by sa[m, g] * sw[n / 128, g] and accumulated in fp32;
+// bias and bf16 rounding happen in the epilogue.
 //
 // Structure (one workgroup = 8 waves, 4 along N x 2 along M, 64 x 128 each):
 //   * Stage = one 128-K group: the 256 x 128-byte weight tile and the 256 x
@@ -23,10 +23,19 @@
 //     not treat them as reads that may alias the in-flight direct-to-LDS
 //     loads of the next stage (it would otherwise wait for those loads before
 //     every fragment read and serialize the pipeline).
-//   * 32x32 output layout: lane l, register r -> n = 8 (r/4) + 4 (l/32) + r%4,
-//     m = l % 32: one token per lane, so the promotion factor is one scalar.
+//   * A wave's step: four weight fragments (16 rows x 128 K each) read once,
+//     then eight 16-token blocks j, each one activation fragment and four
+//     MFMAs.  The fragment of block j + 1 is read while block j's MFMAs run
+//     (a partial lgkmcnt wait), and block j - 1 is promoted after block j's
+//     MFMAs are issued, so the promotion FMAs never wait on the MFMA they
+//     follow.  When all of a wave's token blocks are live the step is
+//     straight-line code, which the scheduler interleaves freely.
+//   * 16x16 output layout: lane l, register r -> n = 4 (l/16) + r, m = l % 16:
+//     one token per lane, so the promotion factor is one scalar per block.
 
 #include <mutex>
+#include <type_traits>
+#include <utility>
 
 #include "gk_fp8_tile.h"
 
@@ -34,6 +43,12 @@ namespace gk {
 
 namespace {
 
+#ifndef GK_PREFILL_SPREAD
+#define GK_PREFILL_SPREAD 1  // a step's tile loads are issued between its token blocks, not all at its top
+#endif
+#ifndef GK_PREFILL_BBUF
+#define GK_PREFILL_BBUF 2  // activation fragments held per wave: reads run one block ahead
+#endif
 constexpr int kBN = 256, kBM = 256;        // workgroup tile (weight rows x tokens)
 constexpr int kTile = 256 * 128;           // one operand tile of one group in LDS
 constexpr int kWStages = 3, kAStages = 2;  // weight / activation stages
@@ -62,16 +77,46 @@ __device__ inline v8i lds_frag(uint32_t a0, uint32_t a1) {
   return r;
 }
 
+// ds_read_b128 at a per-lane base address plus an immediate offset (the
+// instruction's 16-bit offset field): the block offsets of a step cost no
+// address arithmetic.
+template <int OFF>
+__device__ inline u32x4 lds_read16_at(uint32_t base) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(base), "n"(OFF));
+  return r;
+}
+
+template <int OFF>
+__device__ inline v8i lds_frag_at(uint32_t base0, uint32_t base1) {
+  const u32x4 lo = lds_read16_at<OFF>(base0), hi = lds_read16_at<OFF>(base1);
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+
+// f(integral_constant<int, J>) for J = 0, 1, ...: a loop whose index is a
+// compile-time constant in the body (immediate offsets, register arrays).
+template <typename F, int... J>
+__device__ inline void unroll_each(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+
 __device__ inline v8i half_codes(v8i v) {  // native_half: OCP codes -> value / 2 (codec_half4)
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = static_cast<int>(codec_half4(static_cast<uint32_t>(v[i])));
   return v;
 }
 
-__device__ inline void promote(v16f& acc, const v16f& t, float f) {
+__device__ inline void promote4(v4f& acc, const v4f& t, float f) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = fmaf(t[r], f, acc[r]);
+  for (int r = 0; r < 4; ++r) acc[r] = fmaf(t[r], f, acc[r]);
 }
+
+// s_waitcnt lgkmcnt(N) tied to the registers of `v`, so the compiler places
+// their uses after it.
+#define GK_LGKM_WAIT(N, v) asm volatile("s_waitcnt lgkmcnt(" #N ")" : "+v"(v))
 
 // Grouped (MoE) form: the rows of qa are expert segments starting at
 // group_off[e] (multiples of 256, group_off[n_groups] = rows in use) with
@@ -104,7 +149,12 @@ __device__ inline void promote(v16f& acc, const v16f& t, float f) {
 // each loader instruction copies 1 KB of contiguous global memory (wave w:
 // blocks 2w and 2w + 1), and a fragment's two chunks (fc, fc + 1) are the
 // pieces h = 0, 1 of one lane slot, 1024 bytes apart.
-template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false>
+//
+// NA: 16-row weight blocks per wave; the tile is 64 NA weight rows (256, or
+// 192 for the narrow tiles that fill the last round of a large GEMM).  A
+// 48-row wave can straddle two 128-row scale blocks, so NA = 3 takes one
+// weight scale per block.
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -121,11 +171,12 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
   const int wn = wave & 3, wm = wave >> 2;
+  constexpr int BN = 64 * NA;  // weight rows of the tile
   const int tiles_m = Mpad / kBM;
-  const int tiles = tiles_m * ((N + kBN - 1) / kBN);
+  const int tiles = tiles_m * ((N + BN - 1) / BN);
   const int part = static_cast<int>(blockIdx.x) / tiles, bid = static_cast<int>(blockIdx.x) % tiles;
   const int tn = bid / tiles_m, tm = bid % tiles_m;
-  const int n0 = tn * kBN, m0 = tm * kBM;  // consecutive workgroups share the weight panel
+  const int n0 = tn * BN, m0 = tm * kBM;  // consecutive workgroups share the weight panel
   int live = M - m0;                       // rows of this tile whose outputs are used
   if (GROUPED) {
     if (m0 >= group_off[n_groups]) return;  // uniform across the workgroup
@@ -135,18 +186,19 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     sw += e * sw_stride;
     live = min(live, group_cnt[e] - (m0 - group_off[e]));
   }
-  // 32-row blocks of this wave's 128 rows that hold live rows (wave-uniform)
-  const int jlive = min(4, max(0, (live - wm * 128 + 31) / 32));
   const int gbeg = (G * part) / kparts, gend = (G * (part + 1)) / kparts;
 
-  // Loader: wave w fills weight rows and activation rows [32 w, 32 w + 32) of
-  // the stage, 4 + 4 instructions of 8 rows; lane -> (row r0 + 8 i, slot ls)
-  // fetches chunk ls ^ key(row).  Weight rows past N re-read row N-1.
+  // Loader: wave w fills weight rows [8 NA w, +8 NA) and activation rows
+  // [32 w, +32) of the stage, NA + 4 instructions of 8 rows; lane -> (row
+  // r + 8 i, slot ls) fetches chunk ls ^ key(row).  Weight rows past N re-read
+  // row N-1.
   const int lr = lane >> 3, ls = lane & 7;
-  const int r0 = wave * 32 + lr;
-  int lcs[4];
+  const int r0 = wave * 32 + lr, rw0 = wave * 8 * NA + lr;
+  int lcs[4], lcw[NA];
 #pragma unroll
   for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ (((r0 + 8 * i) >> 1) & 7)) * 16;
+#pragma unroll
+  for (int i = 0; i < NA; ++i) lcw[i] = (ls ^ (((rw0 + 8 * i) >> 1) & 7)) * 16;
   // Loader addresses: a wave-uniform base (scalar registers) plus a per-lane
   // 32-bit offset.  Packed weights need one lane offset (lane * 16) and the
   // group-major activations two (the chunk key of rows r0 + 8 i alternates with
@@ -158,12 +210,11 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const int nblk = ((N + 15) >> 4) - 1 - (n0 >> 4);  // last 16-row block of the panel
   const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;
   const uint32_t bl0 = lr * 128 + ((ls ^ (lr >> 1)) << 4), bl1 = lr * 128 + ((ls ^ (lr >> 1) ^ 4) << 4);
-  uint32_t aoff[4], boff[4];
+  uint32_t aoff[NA], boff[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    aoff[i] = static_cast<uint32_t>(min(r0 + 8 * i, nmax) * K + lcs[i]);
-    boff[i] = static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i]);
-  }
+  for (int i = 0; i < NA; ++i) aoff[i] = static_cast<uint32_t>(min(rw0 + 8 * i, nmax) * K + lcw[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) boff[i] = static_cast<uint32_t>(min(r0 + 8 * i, mmax) * ldq + lcs[i]);
   // Activation rows [32 wave, +32) past the tile's live rows are never read
   // (every wave skips its 32-row blocks past them): their copies are skipped.
   const bool act_live = wave * 32 < live;  // wave-uniform
@@ -177,22 +228,40 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(asrc), 0, -1, kBufferWord3);
   const __amdgpu_buffer_rsrc_t arsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(bsrc), 0, -1, kBufferWord3);
-  // Exactly four load instructions each: the step's wait counts on it.
-  auto issue_w = [&](int g, int ws) {
-    uint8_t* base = smem + ws * kTile + wave * 32 * 128;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t vo, so;
-      if (WPACK) {  // block 2 wave + i/2 of the tile (blocks past the last re-read the last one), half i % 2
-        const int blk = min(2 * wave + (i >> 1), nblk);
-        vo = lane16;
-        so = static_cast<uint32_t>((blk * gs + g) * 2048 + (i & 1) * 1024);
-      } else {
-        vo = aoff[i];
-        so = static_cast<uint32_t>(g) * 128u;
-      }
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, lds_ptr(base + i * 1024), 16, vo, so, 0, 0);
+  // Exactly NA weight and four activation load instructions a step: the
+  // step's wait counts on it.  Packed weights: wave w copies the 1 KB pieces
+  // p = NA w + i of the tile (block p / 2, half p % 2; blocks past the last
+  // re-read the last one).
+  auto issue_w_one = [&](int g, int ws, int i) {
+    uint8_t* base = smem + ws * kTile + wave * 8 * NA * 128;
+    uint32_t vo, so;
+    if (WPACK) {
+      const int p = NA * wave + i;
+      const int blk = min(p >> 1, nblk);
+      vo = lane16;
+      so = static_cast<uint32_t>((blk * gs + g) * 2048 + (p & 1) * 1024);
+    } else {
+      vo = aoff[i];
+      so = static_cast<uint32_t>(g) * 128u;
     }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, lds_ptr(base + i * 1024), 16, vo, so, 0, 0);
+  };
+  auto issue_a_one = [&](int g, int as, int i) {
+    if (!act_live) return;
+    uint8_t* base = smem + (kWStages + as) * kTile + wave * 32 * 128;
+    uint32_t vo, so;
+    if (CH) {
+      vo = boff[i];
+      so = static_cast<uint32_t>(g) * 128u;
+    } else {
+      vo = (i & 1) ? bl1 : bl0;
+      so = static_cast<uint32_t>(g) * static_cast<uint32_t>(Mpad * 128) + static_cast<uint32_t>((wave * 32 + 8 * i) * 128);
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, lds_ptr(base + i * 1024), 16, vo, so, 0, 0);
+  };
+  auto issue_w = [&](int g, int ws) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) issue_w_one(g, ws, i);
   };
   auto issue_a = [&](int g, int as) {
     if (!act_live) return;
@@ -211,63 +280,74 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     }
   };
 
-  // Fragments: lane -> row (lane & 31) of a 32-row strip, chunks h*4 + 2 (lane >> 5) + {0, 1}.
-  const int fr = lane & 31, fc = (lane >> 5) * 2, kf = (fr >> 1) & 7;
-  const uint32_t xo00 = ((0 + fc) ^ kf) << 4, xo01 = ((1 + fc) ^ kf) << 4;
-  const uint32_t xo10 = ((4 + fc) ^ kf) << 4, xo11 = ((5 + fc) ^ kf) << 4;
-  // packed weight tile: row ra = wn*64 + fr, chunk fc + h (+4 for the second K half) ->
-  // (ra/16)*2048 + h*1024 + 16*(16*((fc + 4k)/2) + ra%16)
-  const uint32_t pa = ((wn * 64 + fr) >> 4) * 2048 + 16 * (16 * (lane >> 5) + (fr & 15));
-  const uint32_t ya00 = WPACK ? 0u : xo00, ya01 = WPACK ? 1024u : xo01;
-  const uint32_t ya10 = WPACK ? 512u : xo10, ya11 = WPACK ? 1536u : xo11;
+  // Fragments (16x16x128 operand layout): lane -> row (lane & 15) of a
+  // 16-row block, K bytes [32 (lane >> 4), +32) = chunks 2 (lane >> 4) + {0, 1}.
+  // Row-major tiles keep chunk c of row r at slot c ^ ((r >> 1) & 7); the
+  // packed weight tile holds each 16-row block as 2 KB in fragment order
+  // (piece h of lane l at h * 1024 + 16 l).
+  const int fr = lane & 15, fq = lane >> 4, kf = (fr >> 1) & 7;
+  const uint32_t xo0 = static_cast<uint32_t>(((2 * fq) ^ kf) << 4), xo1 = static_cast<uint32_t>(((2 * fq + 1) ^ kf) << 4);
   const uint32_t lbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
-  const uint32_t arow = WPACK ? pa : (wn * 64 + fr) * 128, brow = kWStages * kTile + (wm * 128 + fr) * 128;
-  const float* sap = sa + (m0 + wm * 128 + fr);  // + 32 j + g * Mpad  (m0 + 256 <= Mpad)
-  const float* swp = sw + static_cast<int64_t>(min(n0 + wn * 64, N - 1) >> 7) * gs;
+  // weight block i of this wave: rows wn*16*NA + 16 i
+  const uint32_t arow = WPACK ? static_cast<uint32_t>(wn * NA * 2048 + 16 * lane)
+                              : static_cast<uint32_t>((wn * 16 * NA + fr) * 128);
+  const uint32_t ya0 = WPACK ? 0u : xo0, ya1 = WPACK ? 1024u : xo1;
+  // activation block j of this wave: tokens wm*128 + 16 j
+  const uint32_t brow = static_cast<uint32_t>(kWStages * kTile + (wm * 128 + fr) * 128);
+  const float* sap = sa + (m0 + wm * 128 + fr);  // + 16 j + g * Mpad  (m0 + 256 <= Mpad)
+  // weight scale rows of the wave's blocks (one for NA = 4: 64 rows at a multiple of 64)
+  constexpr int kScales = NA == 4 ? 1 : NA;
+  const float* swp[kScales];
+#pragma unroll
+  for (int i = 0; i < kScales; ++i)
+    swp[i] = sw + static_cast<int64_t>(min(n0 + wn * 16 * NA + 16 * i, N - 1) >> 7) * gs;
   float* ypp = yp ? yp + static_cast<int64_t>(part) * M * ldyp : nullptr;
+  // 16-token blocks of this wave's 128 rows that hold live rows (wave-uniform)
+  const int jl = min(8, max(0, (live - wm * 128 + 15) / 16));
 
-  // Accumulator element (i, j, 4 q + r) is output (m0 + wm*128 + 32 j + fr,
-  // n0 + wn*64 + 32 i + 8 q + 4 (lane/32) + r).  With accum the sums start
-  // from the fp32 partial in yp, so K ranges accumulated over several calls
-  // give the bits of one call over their union.
-  v16f acc[2][4];
+  // Accumulator acc[i][j] register r is output (m0 + wm*128 + 16 j + fr,
+  // n0 + wn*16*NA + 16 i + 4 fq + r).  With accum the sums start from the fp32
+  // partial in yp, so K ranges accumulated over several calls give the bits
+  // of one call over their union.
+  v4f acc[NA][8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < NA; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   if (accum) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 8; ++j) {
+      const int m = m0 + wm * 128 + j * 16 + fr;
+      if (j >= jl || m >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 128 + j * 32 + fr;
-        if (j >= jlive || m >= M) continue;
+      for (int i = 0; i < NA; ++i) {
+        const int n = n0 + wn * 16 * NA + i * 16 + 4 * fq;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < N) acc[i][j][4 * q + r] = ypp[static_cast<int64_t>(m) * ldyp + n + r];
-        }
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) acc[i][j][r] = ypp[static_cast<int64_t>(m) * ldyp + n + r];
       }
+    }
   }
 
   // Issue order in step g: token scales of g + 1 (before the wait), then, past
   // the barrier, activations of g + 1 and weights of g + 2.  Weights are issued
   // at every step (past the last group they re-read it into a stage no later
   // step reads), so at the top of step g the loads younger than step g's
-  // activations are exactly weights g + 1 and scales g + 1: vmcnt(8) (vmcnt(4)
+  // activations are exactly weights g + 1 and scales g + 1: vmcnt(12) (vmcnt(4)
   // in the CH form, which loads no token scales) completes step g's tiles and
   // leaves those in flight.  The compiler tracks the scale loads itself; it
   // counts the buffer loads exactly, so its waits for them are partial too.
-  float sv[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // token scales of the next step
+  float sv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};  // token scales of the next step
   auto load_sav = [&](int g) {
     if (!CH) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sv[j] = sap[j * 32 + static_cast<int64_t>(g) * Mpad];
+      for (int j = 0; j < 8; ++j) sv[j] = sap[j * 16 + static_cast<int64_t>(g) * Mpad];
     }
+  };
+  // One token block: NA MFMAs on the weight fragments.
+  auto block_mfma = [&](const v8i (&a)[NA], const v8i& b, v4f (&t)[NA]) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) t[i] = mfma_f8(a[i], b);
   };
   // (An empty K range, a K-split half with no groups, stores zeros.)
   if (gbeg < gend) {
@@ -279,61 +359,105 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     int g = gbeg;
     do {
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
-      const float swg = CH ? 0.0f : (HALF ? 2.0f * swp[g] : swp[g]);
-      float fj[4];  // promotion factors of step g
+      float swg[NA];  // weight scales of step g (promotion factor of block (i, j): svg[j] * swg[i])
 #pragma unroll
-      for (int j = 0; j < 4; ++j) fj[j] = sv[j] * swg;
+      for (int i = 0; i < NA; ++i) {
+        const float v = CH ? 0.0f : swp[i < kScales ? i : 0][g];
+        swg[i] = HALF ? 2.0f * v : v;
+      }
+      float svg[8];  // token scales of step g
+#pragma unroll
+      for (int j = 0; j < 8; ++j) svg[j] = sv[j];
       load_sav(min(g + 1, gend - 1));
       asm volatile("" ::: "memory");  // the scale loads stay ahead of the wait, whose count includes them
-      // This wave's tile loads of step g are done: vmcnt(8) or vmcnt(4), expcnt(7), lgkmcnt(15).
-      if (CH)
-        __builtin_amdgcn_s_waitcnt(0x0F74);
-      else
-        __builtin_amdgcn_s_waitcnt(0x0F78);
+      // This wave's tile loads of step g are done: vmcnt(8 + NA) or vmcnt(NA), expcnt(7), lgkmcnt(15).
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (CH ? NA : 8 + NA));
       // ... for every wave; all fragment reads of step g-1 are done too (each
       // step's reads end with lgkmcnt(0)).  A bare barrier: __syncthreads()'s
       // release fence would wait for the weight loads still in flight.
       __builtin_amdgcn_s_barrier();
-      if (g + 1 < gend) issue_a(g + 1, as ^ 1);
-      issue_w(min(g + 2, gend - 1), ws == 0 ? 2 : ws - 1);  // the stage step g-1 used
+      const int as_next = as ^ 1, ws_free = ws == 0 ? 2 : ws - 1;  // the stages step g-1 used
+      if (!GK_PREFILL_SPREAD) {
+        if (g + 1 < gend) issue_a(g + 1, as_next);
+        issue_w(min(g + 2, gend - 1), ws_free);
+      }
       const uint32_t A = lbase + ws * kTile + arow;
       const uint32_t B = lbase + as * kTile + brow;
       ws = ws == 2 ? 0 : ws + 1;
       as ^= 1;
-      if (jlive == 0) continue;  // no live rows for this wave (it still takes part in the loads and barriers)
-      v8i a00 = lds_frag(A + ya00, A + ya01), a01 = lds_frag(A + ya10, A + ya11);
-      v8i a10 = lds_frag(A + 4096 + ya00, A + 4096 + ya01), a11 = lds_frag(A + 4096 + ya10, A + 4096 + ya11);
-      v8i b0 = lds_frag(B + xo00, B + xo01), b1 = lds_frag(B + xo10, B + xo11);
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a00), "+v"(a01), "+v"(a10), "+v"(a11), "+v"(b0), "+v"(b1));
-      if (HALF) {
-        a00 = half_codes(a00); a01 = half_codes(a01); a10 = half_codes(a10); a11 = half_codes(a11);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < jlive) {  // wave-uniform; j is a constant after unrolling, so acc stays in registers
-          if (j > 0) {
-            b0 = lds_frag(B + j * 4096 + xo00, B + j * 4096 + xo01);
-            b1 = lds_frag(B + j * 4096 + xo10, B + j * 4096 + xo11);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(b1));
-          }
-          if (CH) {
-            acc[0][j] = mfma32_f8(a00, b0, acc[0][j]);
-            acc[1][j] = mfma32_f8(a10, b0, acc[1][j]);
-            acc[0][j] = mfma32_f8(a01, b1, acc[0][j]);
-            acc[1][j] = mfma32_f8(a11, b1, acc[1][j]);
-          } else {
-            const float f = fj[j];
-            v16f t;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) t[r] = 0.0f;
-            t = mfma32_f8(a01, b1, mfma32_f8(a00, b0, t));
-            promote(acc[0][j], t, f);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) t[r] = 0.0f;
-            t = mfma32_f8(a11, b1, mfma32_f8(a10, b0, t));
-            promote(acc[1][j], t, f);
+      // A wave with no live rows skips its MFMAs (GROUPED: every block; dense
+      // GEMMs, where only the last row tile has such waves, compute them and
+      // never store them), but runs the step: it copies its share of the next
+      // tiles there.
+      if (jl == 0 && !GK_PREFILL_SPREAD) continue;
+      // Straight-line step.  b[j % kNB] holds block j's fragment; reads run kNB - 1
+      // blocks ahead of the MFMAs, and block j - 1 is promoted after block j's
+      // MFMAs are issued.  Token blocks past the live rows are computed too
+      // (their rows of the tile are zeros or stale LDS contents, which only
+      // reach their own outputs, never stored): one code path keeps the
+      // accumulators in registers.  Block offsets are immediates of the reads.
+      const uint32_t A0 = A + ya0, A1 = A + ya1, B0 = B + xo0, B1 = B + xo1;
+      v8i a[NA];
+      unroll_each([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        a[i] = lds_frag_at<i * 2048>(A0, A1);  // 16 weight rows = 2 KB in both tile layouts
+      }, std::make_integer_sequence<int, NA>{});
+      constexpr int kNB = GK_PREFILL_BBUF;
+      static_assert(kNB >= 2 && kNB <= 8, "activation fragment buffers");
+      v8i b[kNB];
+      unroll_each([&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        b[u] = lds_frag_at<u * 2048>(B0, B1);
+      }, std::make_integer_sequence<int, kNB - 1>{});
+      v4f t[2][NA];
+      unroll_each([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        // Expert segments (GROUPED) often end inside a wave's rows: there the
+        // blocks past the live rows are skipped (a wave-uniform branch).  Dense
+        // GEMMs have at most one partial row tile and keep the branch-free step.
+        const bool skip = GROUPED && j >= jl;
+        if (GK_PREFILL_SPREAD) {  // this step's tile loads, spread over the first blocks
+          if (j < 4) {
+            if (g + 1 < gend) issue_a_one(g + 1, as_next, j);
+          } else if (j - 4 < NA) {
+            issue_w_one(min(g + 2, gend - 1), ws_free, j - 4);
           }
         }
+        // block j + kNB - 1's read goes out; then block j's fragment must be in,
+        // with the reads of blocks j + 1 .. min(7, j + kNB - 1) still in flight
+        if (j + kNB - 1 < 8) b[(j + kNB - 1) % kNB] = lds_frag_at<(j + kNB - 1) * 2048>(B0, B1);
+        constexpr int later = (kNB - 1 < 7 - j) ? kNB - 1 : 7 - j;
+        if (j == 0) {  // ... and the weight fragments, read before block 0's
+          asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a[0]), "+v"(a[NA - 1]), "+v"(b[0]) : "n"(2 * later));
+          if (NA == 4) asm volatile("" : "+v"(a[1]), "+v"(a[2]));
+          if (NA == 3) asm volatile("" : "+v"(a[1]));
+          if (HALF) {
+#pragma unroll
+            for (int i = 0; i < NA; ++i) a[i] = half_codes(a[i]);
+          }
+        } else {
+          asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(b[j % kNB]) : "n"(2 * later));
+        }
+        if (CH) {
+#pragma unroll
+          for (int i = 0; i < NA; ++i) acc[i][j] = mfma_f8_acc(a[i], b[j % kNB], acc[i][j]);
+        } else if (GROUPED) {
+          if (!skip) {
+            block_mfma(a, b[j % kNB], t[0]);
+#pragma unroll
+            for (int i = 0; i < NA; ++i) promote4(acc[i][j], t[0][i], svg[j] * swg[i]);
+          }
+        } else {
+          block_mfma(a, b[j % kNB], t[j & 1]);
+          if (j > 0) {
+#pragma unroll
+            for (int i = 0; i < NA; ++i) promote4(acc[i][j - 1], t[(j - 1) & 1][i], svg[j - 1] * swg[i]);
+          }
+        }
+      }, std::make_integer_sequence<int, 8>{});
+      if (!CH && !GROUPED) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) promote4(acc[i][7], t[1][i], svg[7] * swg[i]);
       }
     } while (++g < gend);
   }
@@ -342,22 +466,19 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 
   if (CH) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < jlive) {
-        const int m = m0 + wm * 128 + j * 32 + fr;
+    for (int j = 0; j < 8; ++j) {
+      if (j < jl) {
+        const int m = m0 + wm * 128 + j * 16 + fr;
         if (m < M) {
           const float sam = sa[m];
           uint16_t* row = y + static_cast<int64_t>(m) * ldy;
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < NA; ++i) {
+            const int n = n0 + wn * 16 * NA + i * 16 + 4 * fq;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (n + r < N)
-                  row[n + r] = channel_out(acc[i][j][4 * q + r], sam, sw[n + r], bias ? bias[n + r] : 0.0f);
-            }
+            for (int r = 0; r < 4; ++r)
+              if (n + r < N) row[n + r] = channel_out(acc[i][j][r], sam, sw[n + r], bias ? bias[n + r] : 0.0f);
+          }
         }
       }
     }
@@ -365,77 +486,120 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   }
   if (yp) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 8; ++j) {
+      if (j < jl) {
+        const int m = m0 + wm * 128 + j * 16 + fr;
+        if (m >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < jlive) {
+        for (int i = 0; i < NA; ++i) {
+          const int n = n0 + wn * 16 * NA + i * 16 + 4 * fq;
+          float* dst = ypp + static_cast<int64_t>(m) * ldyp + n;
+          const v4f v = acc[i][j];
+          if (n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+            *reinterpret_cast<v4f*>(dst) = v;
+          } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int m = m0 + wm * 128 + j * 32 + fr, n = n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5);
-            if (m >= M) continue;
-            float* dst = ypp + static_cast<int64_t>(m) * ldyp + n;
-            const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-            if (n + 3 < N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-              *reinterpret_cast<v4f*>(dst) = v;
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (n + r < N) dst[r] = v[r];
-            }
+            for (int r = 0; r < 4; ++r)
+              if (n + r < N) dst[r] = v[r];
           }
         }
       }
+    }
     return;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < 8; ++j) {
+    if (j < jl) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < jlive) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const v4f v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-          store_tile(y, ldy, bias, M, N, m0 + wm * 128 + j * 32 + fr,
-                     n0 + wn * 64 + i * 32 + 8 * q + 4 * (lane >> 5), v);
-        }
-      }
+      for (int i = 0; i < NA; ++i)
+        store_tile(y, ldy, bias, M, N, m0 + wm * 128 + j * 16 + fr, n0 + wn * 16 * NA + i * 16 + 4 * fq, acc[i][j]);
     }
+  }
 }
 
-// The 128 KB of dynamic LDS is above the default limit: raise it once per device.
+// The 160 KB of dynamic LDS is above the default limit: raise it once per device.
 constexpr int kMaxDevices = 64;
 
-std::once_flag g_lds_once[kMaxDevices][16];
-hipError_t g_lds_err[kMaxDevices][16];
+std::once_flag g_lds_once[kMaxDevices][32];
+hipError_t g_lds_err[kMaxDevices][32];
 
-template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false>
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
 hipError_t ensure_lds_limit() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0) + (WPACK ? 8 : 0);
+  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0) + (WPACK ? 8 : 0) + (NA == 3 ? 16 : 0);
   std::call_once(g_lds_once[dev][slot], [dev] {
     g_lds_err[dev][slot] = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH, WPACK>),
+        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH, WPACK, NA>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   });
   return g_lds_err[dev][slot];
 }
 
-template <bool HALF, bool GROUPED, bool WPACK = false>
+template <bool HALF, bool GROUPED, bool WPACK = false, int NA = 4>
 hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
                      int64_t w_stride, int64_t sw_stride, int kparts, float* yp, int64_t ldyp, hipStream_t stream) {
-  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK>();
+  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK, NA>();
   if (e != hipSuccess) return e;
-  const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (a.Mpad / kBM));
-  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK><<<tiles * kparts, 512, kLdsBytes, stream>>>(
+  constexpr int BN = 64 * NA;
+  const unsigned tiles = static_cast<unsigned>(((a.N + BN - 1) / BN) * (a.Mpad / kBM));
+  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK, NA><<<tiles * kparts, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
       w_stride, sw_stride, kparts, yp, 0, a.gstride(), ldyp, a.accumulate ? 1 : 0);
   return hipGetLastError();
 }
 
+template <int NA>
+hipError_t launch_dense(const GemmArgs& a, hipStream_t stream) {
+  if (a.wpack)
+    return a.half_w ? launch256<true, false, true, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
+                    : launch256<false, false, true, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
+  return a.half_w ? launch256<true, false, false, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
+                  : launch256<false, false, false, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
+}
+
+// Compute units of the current device (cached per device; 0 if unknown).
+std::once_flag g_cu_once[kMaxDevices];
+int g_cus[kMaxDevices];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  std::call_once(g_cu_once[dev], [dev] {
+    int n = 0;
+    g_cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? n : 0;
+  });
+  return g_cus[dev];
+}
+
 }  // namespace
+
+// Columns [0, n_wide) in 256-wide weight tiles and the rest in 192-wide tiles,
+// when that fills the CUs better than 256-wide tiles alone: a GEMM whose
+// 256 x 256 tiles need more than one round over the CUs otherwise leaves CUs
+// idle in its last round (config 4: 448 tiles on 256 CUs = 1.75 rounds, run
+// as 256 + 256 tiles of 256 and 192 columns).  Work is counted in rounds, a
+// 192-wide tile taking 0.8 of a 256-wide one (it keeps the activation
+// traffic of the full tile).  Returns N (no split) when nothing gains.
+int prefill_wide_columns(int Mpad, int N, int cus) {
+  const int tiles_m = Mpad / kBM;
+  const int nt = (N + 255) / 256;
+  if (cus <= 0 || tiles_m * nt <= cus) return N;
+  auto rounds = [cus](int tiles) { return (tiles + cus - 1) / cus; };
+  double best = rounds(tiles_m * nt);
+  int best_wide = N;
+  for (int a = 1; a < nt; ++a) {
+    const int n2 = N - 256 * a;
+    const double est = rounds(tiles_m * a) + 0.8 * rounds(tiles_m * ((n2 + 191) / 192)) + 0.02;
+    if (est < best - 1e-9) {
+      best = est;
+      best_wide = 256 * a;
+    }
+  }
+  return best_wide;
+}
 
 // Per-token / per-channel form: a.qa row-major [M][a.ldq], a.sa [M], a.sw [N]; any M.
 hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
@@ -452,14 +616,29 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
 }
 
 // Requires K % 128 == 0, 16-byte aligned weights, Mpad % 256 == 0 (qa/sa
-// padded with zero rows up to Mpad).
+// padded with zero rows up to Mpad).  Large GEMMs may run as two launches
+// over column ranges (prefill_wide_columns); each output column is computed
+// by one workgroup either way, with the same per-element arithmetic.
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
   if (a.Mpad % kBM != 0 || !prefill256_fits(a)) return hipErrorInvalidValue;
-  if (a.wpack)
-    return a.half_w ? launch256<true, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
-                    : launch256<false, false, true>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
-  return a.half_w ? launch256<true, false>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
-                  : launch256<false, false>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
+  const int wide = prefill_wide_columns(a.Mpad, a.N, device_cus());
+  if (wide >= a.N) return launch_dense<4>(a, stream);
+  hipError_t e = launch_dense<4>([&] {
+    GemmArgs w = a;
+    w.N = wide;
+    return w;
+  }(), stream);
+  if (e != hipSuccess) return e;
+  // Columns [wide, N): weight rows from `wide` (row-major: + wide * K bytes; packed:
+  // 16-row tiles of gs * 2048 = K * 16 bytes, the same offset), scale rows from wide / 128.
+  GemmArgs r = a;
+  r.N = a.N - wide;
+  r.w = a.w + static_cast<int64_t>(wide) * a.K;
+  r.sw = a.sw + static_cast<int64_t>(wide / 128) * a.gstride();
+  if (a.bias) r.bias = a.bias + wide;
+  if (a.y) r.y = a.y + wide;
+  if (a.yp) r.yp = a.yp + wide;
+  return launch_dense<3>(r, stream);
 }
 
 // Grouped form: a.Mpad = padded rows (multiple of 256), a.M = a.Mpad; weights
