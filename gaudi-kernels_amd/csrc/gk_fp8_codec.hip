@@ -152,37 +152,51 @@ __global__ __launch_bounds__(256) void codec_scales_kernel(const float* __restri
 // x: bf16 [M, K] with row stride ldx (elements).  Group-major outputs (the
 // reference quant op's {128, R, G} layout): q [G][Mpad][128] codes (rows >= M
 // and columns >= K are written as zero), sa [G][Mpad] fp32 (zero for rows >=
-// M).  One group = 16 lanes x 8 elements (quant_group8).  PACKED writes q in
-// the decode fragment layout instead (Mpad = 16, 32 or 64; gk_fp8_internal.h).
-template <bool HALF, bool PACKED>
+// M).  One group = 16 lanes x 8 elements (quant_group8); each 16-lane set
+// takes U consecutive groups and issues their loads before quantizing any
+// (bytes in flight: the kernel streams ~1.5 B per element).  PACKED writes q
+// in the decode fragment layout instead (Mpad = 16, 32 or 64;
+// gk_fp8_internal.h).
+template <bool HALF, bool PACKED, int U>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                         int K, int G, int Mpad, uint8_t* __restrict__ q,
                                                         float* __restrict__ sa, int vec_ok) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const int64_t gid0 = (static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4)) * U;
   const int sub = threadIdx.x & 15;
   const int64_t total = static_cast<int64_t>(Mpad) * G;
-  const bool active = gid < total;
-  const int64_t row = active ? gid / G : 0;
-  const int g = active ? static_cast<int>(gid - row * G) : 0;
-  const int col = g * 128 + sub * 8;
-  const bool live = active && row < M;
-  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-  if (live && col + 8 <= K && vec_ok) {
-    raw = *reinterpret_cast<const uint4*>(x + row * ldx + col);
-  } else if (live) {
-    uint32_t h[8];
+  uint4 raw[U];
+  int64_t row[U];
+  int gg[U];
+  bool active[U], live[U];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = (col + i < K) ? x[row * ldx + col + i] : 0u;
-    raw = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+  for (int u = 0; u < U; ++u) {
+    const int64_t gid = gid0 + u;
+    active[u] = gid < total;
+    row[u] = active[u] ? gid / G : 0;
+    gg[u] = active[u] ? static_cast<int>(gid - row[u] * G) : 0;
+    const int col = gg[u] * 128 + sub * 8;
+    live[u] = active[u] && row[u] < M;
+    raw[u] = make_uint4(0u, 0u, 0u, 0u);
+    if (live[u] && col + 8 <= K && vec_ok) {
+      raw[u] = *reinterpret_cast<const uint4*>(x + row[u] * ldx + col);
+    } else if (live[u]) {
+      uint32_t h[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h[i] = (col + i < K) ? x[row[u] * ldx + col + i] : 0u;
+      raw[u] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    }
   }
-  float s;
-  const uint2 codes = quant_group8(raw, live, HALF, &s);  // all 16 lanes of a group take part
-  if (active) {
-    const int64_t slot = static_cast<int64_t>(g) * Mpad + row;
-    // bytes [8 sub, 8 sub + 8): 16-byte chunk c = sub / 2 goes to piece (c % 2, 16 (c / 2) + row)
-    const int64_t at = PACKED ? decode_layout_offset(g, row, 8 * sub, Mpad) : slot * 128 + sub * 8;
-    *reinterpret_cast<uint2*>(q + at) = live ? codes : make_uint2(0u, 0u);
-    if (sub == 0) sa[slot] = live ? s : 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float s;
+    const uint2 codes = quant_group8(raw[u], live[u], HALF, &s);  // all 16 lanes of a group take part
+    if (active[u]) {
+      const int64_t slot = static_cast<int64_t>(gg[u]) * Mpad + row[u];
+      // bytes [8 sub, 8 sub + 8): 16-byte chunk c = sub / 2 goes to piece (c % 2, 16 (c / 2) + row)
+      const int64_t at = PACKED ? decode_layout_offset(gg[u], row[u], 8 * sub, Mpad) : slot * 128 + sub * 8;
+      *reinterpret_cast<uint2*>(q + at) = live[u] ? codes : make_uint2(0u, 0u);
+      if (sub == 0) sa[slot] = live[u] ? s : 0.0f;
+    }
   }
 }
 
@@ -256,9 +270,17 @@ hipError_t launch_act_quant(const uint16_t* x, int64_t ldx, int M, int K, int Mp
   if (packed && Mpad != 16 && Mpad != 32 && Mpad != 64) return hipErrorInvalidValue;
   const int G = (K + 127) / 128;
   const int64_t groups = static_cast<int64_t>(Mpad) * G;
-  const int blocks = static_cast<int>((groups + 15) / 16);  // 16 groups per 256-thread block
   const int vec_ok = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (ldx % 8 == 0);
-#define GK_AQ(H, P) act_quant_kernel<H, P><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok)
+  // Four groups per 16 lanes once there are enough groups to keep every CU
+  // busy with them (prefill-sized inputs); decode-sized inputs keep one.
+  const bool wide = groups >= 65536;
+  const int per = wide ? 64 : 16;  // groups per 256-thread block
+  const int blocks = static_cast<int>((groups + per - 1) / per);
+#define GK_AQ(H, P)                                                                                          \
+  do {                                                                                                       \
+    if (wide) act_quant_kernel<H, P, 4><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok);     \
+    else act_quant_kernel<H, P, 1><<<blocks, 256, 0, stream>>>(x, ldx, M, K, G, Mpad, q, sa, vec_ok);          \
+  } while (0)
   if (half) {
     if (packed) GK_AQ(true, true); else GK_AQ(true, false);
   } else {
