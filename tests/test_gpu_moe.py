@@ -171,6 +171,7 @@ def regions(ws, t, h, inter, e, k):
     for p in range(1, parts):
         z = z + zp[p]                     # fp32, as the combine does
     v["z"] = z.to(torch.bfloat16)
+    v["zp"] = zp.clone()                  # the fp32 planes themselves
     v["parts"] = torch.tensor(parts)
     return {n: x.cpu() for n, x in v.items()}
 
@@ -221,6 +222,28 @@ def test_moe_config5_stagewise_parity():
     for s in range(1, k):
         acc = acc + wts[:, s:s + 1] * z[row_of[:, s]]
     assert torch.equal(y, acc.bfloat16())
+
+
+
+@pytest.mark.timeout(600)
+def test_moe_config5_packed_bit_identical():
+    """Config 5 with experts packed at load time against row-major experts: the gate_up output, the down
+    GEMM's fp32 K-split planes and y agree bit for bit (the grouped kernel's two weight layouts)."""
+    t, h, inter, e, k = 512, 4096, 14336, 8, 2
+    x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=5000, device="cuda")
+    xg, lg = x.cuda(), logits.cuda()
+    nbytes = ops.moe_workspace_bytes(t, h, inter, e, k)
+    ws_row = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    ws_pack = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device="cuda")
+    y_row = ops.moe_block_fp8(xg, lg, wg, sg, wd, sd, top_k=k, workspace=ws_row)
+    y_pack = ops.moe_block_fp8(xg, lg, ops.pack_experts(wg), sg, ops.pack_experts(wd), sd, top_k=k, workspace=ws_pack)
+    torch.cuda.synchronize()
+    r_row, r_pack = regions(ws_row, t, h, inter, e, k), regions(ws_pack, t, h, inter, e, k)
+    rows = r_row["row_of"].long().reshape(-1)  # every routed row
+    assert torch.equal(r_row["row_of"], r_pack["row_of"])
+    assert torch.equal(r_row["hpre"][rows].view(torch.int16), r_pack["hpre"][rows].view(torch.int16))
+    assert torch.equal(r_row["zp"][:, rows].view(torch.int32), r_pack["zp"][:, rows].view(torch.int32))
+    assert torch.equal(y_row.view(torch.int16), y_pack.view(torch.int16))
 
 
 @pytest.mark.timeout(600)
