@@ -49,7 +49,8 @@ MALL_ROTATE_BYTES = 512 << 20
 # launch of it.
 DECODE_KERNEL = "gk::gemm_decode_kernel<8,2,4,false,false,false,true,true,1>"
 # The prefill roofline kernel: the 256 x 256 LDS-tiled MFMA kernel on packed weights (config 4).
-PREFILL_KERNEL = "gk::gemm_prefill256_kernel<false,false,false,true>"
+# config 4 is two launches of this kernel (template argument NA = 4 on 4096 columns, 3 on the other 3072)
+PREFILL_KERNEL = "gk::gemm_prefill256_kernel<false,false,false,true,"
 SIMD_NUM = 1024  # 256 CUs x 4 SIMDs (MI355X)
 
 
@@ -141,27 +142,34 @@ def profile_lines():
 
 
 def measured_traffic(kernel_prefix, workload):
-    """HBM bytes per launch of the kernel whose name starts with `kernel_prefix` on `workload`, from the
-    committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE scaled by a plain-copy calibration),
-    or None if not recorded."""
+    """HBM bytes of one op on `workload`: the sum over the launches of kernels whose names start with
+    `kernel_prefix`, from the committed rocprofv3 --pmc summaries (FETCH_SIZE and WRITE_SIZE scaled by a
+    plain-copy calibration), or None if not recorded."""
     import re
+    total, seen = 0, set()
     for line in profile_lines():
         m = re.match(r"traffic: kernel=(\S+) workload=(\S+) .* bytes=(\d+)", line)
-        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload:
-            return int(m.group(3))
-    return None
+        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload and m.group(1) not in seen:
+            seen.add(m.group(1))
+            total += int(m.group(3))
+    return total if seen else None
 
 
 def measured_mfma(kernel_prefix, workload):
-    """(MFMA busy fraction, F8 MFMA FLOPs per launch, GRBM_GUI_ACTIVE cycles) of the kernel on `workload` from the
-    committed rocprofv3 --pmc summary, or None if not recorded."""
+    """(MFMA busy fraction, F8 MFMA FLOPs, GRBM_GUI_ACTIVE cycles) of one op on `workload` from the committed
+    rocprofv3 --pmc summaries: FLOPs and cycles summed over the launches of kernels whose names start with
+    `kernel_prefix`, the busy fraction weighted by each launch's cycles; None if not recorded."""
     import re
+    busy, flops, cycles, seen = 0.0, 0.0, 0.0, set()
     for line in profile_lines():
         m = re.match(r"mfma: kernel=(\S+) workload=(\S+) .*busy_frac=([0-9.]+) .*f8_flops=([0-9.e+]+) .*gui_cycles=([0-9.]+)",
                      line)
-        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload:
-            return float(m.group(3)), float(m.group(4)), float(m.group(5))
-    return None
+        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload and m.group(1) not in seen:
+            seen.add(m.group(1))
+            busy += float(m.group(3)) * float(m.group(5))
+            flops += float(m.group(4))
+            cycles += float(m.group(5))
+    return (busy / cycles, flops, cycles) if seen and cycles > 0 else None
 
 
 def kernel_short_name(name):
@@ -230,7 +238,7 @@ def rocprof_summary(directory):
                 continue
             f_kib, w_kib = med(v), med(wv)
             total = int(round(f_kib * 1024 * fs + w_kib * 1024 * ws))
-            print(f"traffic: kernel={short.replace(' ', '')} workload={WORKLOAD_BY_GRID.get(grid, 'grid' + grid)} "
+            print(f"traffic: kernel={short.replace(' ', '')} workload={workload_of(short, grid)} "
                   f"grid={grid} fetch_kib={f_kib:.1f} write_kib={w_kib:.1f} fetch_scale={fs:.4f} write_scale={ws:.4f} "
                   f"bytes={total}\n")
     # Matrix-core evidence: MfmaUtil (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, percent),
@@ -243,13 +251,21 @@ def rocprof_summary(directory):
         gui = counters.get((name, grid, "GRBM_GUI_ACTIVE"))
         if not mops or not gui:
             continue
-        print(f"mfma: kernel={short.replace(' ', '')} workload={WORKLOAD_BY_GRID.get(grid, 'grid' + grid)} grid={grid} "
+        print(f"mfma: kernel={short.replace(' ', '')} workload={workload_of(short, grid)} grid={grid} "
               f"busy_frac={med(v) / 100:.4f} f8_flops={med(mops) * 512:.6e} gui_cycles={med(gui):.0f}\n")
 
 
 # Dispatch grids (threads) of the bench workloads' GEMM kernels -> workload names in profile summaries.
 WORKLOAD_BY_GRID = {"98304": "config2", "114688": "config3_gate_up", "131072": "config3_down",
-                    "229376": "config4", "688128": "config5_gate_up", "196608": "config5_down"}
+                    "688128": "config5_gate_up", "196608": "config5_down"}
+
+
+def workload_of(kernel, grid):
+    """Workload of a GEMM dispatch in a profile summary: by grid, except the config 4 prefill launches (both tile
+    widths run 256 workgroups of 512 threads, the grid of config 3's down-projection decode launch)."""
+    if "prefill256" in kernel and grid == "131072":
+        return "config4"
+    return WORKLOAD_BY_GRID.get(grid, "grid" + grid)
 
 
 def copy_calibration():
@@ -705,9 +721,10 @@ def main():
         result["roofline_prefill"] = {
             "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": measured_traffic(PREFILL_KERNEL, "config4"),
-            "kernel": f"{PREFILL_KERNEL} (config 4: M=4096, N=K=7168, packed weights, activations quantized "
-                      "beforehand)",
-            "flops_per_launch": f, "avg_launch_us": round(ms4k * 1e3, 2), "op_frac": round(f / (ms4 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
+            "kernel": f"{PREFILL_KERNEL}NA> (config 4: M=4096, N=K=7168, one op = two launches, NA=4 tiles on "
+                      "4096 columns and NA=3 on 3072; packed weights, activations quantized beforehand)",
+            "flops_per_op": f, "avg_op_us": round(ms4k * 1e3, 2),
+            "op_frac": round(f / (ms4 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
             "counters": None if counters is None else {
                 "mfma_busy_frac": counters[0], "f8_mfma_flops": counters[1], "gui_active_cycles": counters[2],
                 "source": "profiles/prefill_moe_gemm_counters.md (rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_F8 "

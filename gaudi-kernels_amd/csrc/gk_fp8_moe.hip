@@ -157,10 +157,8 @@ __global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __r
 // ---- fused SiLU-and-mul + 1x128 quantization ----------------------------------------
 // h: bf16 [rows, 2*inter] (gate | up); rows past off[E] and padding rows
 // (row_token < 0, whose gate_up outputs were never computed) are skipped.
-// Lane: 8 gate and 8 up values of one 128-column group -> 8 bf16 products ->
-// codes.  A 16-lane set takes U consecutive groups of one row and issues all
-// of their loads before the arithmetic (more bytes in flight per lane).
-template <bool HALF, int U>
+// Lane: 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
+template <bool HALF>
 __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ h, int64_t ldh, int inter,
                                                              int G, const int32_t* __restrict__ off,
                                                              const int32_t* __restrict__ row_token, int E,
@@ -168,37 +166,30 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __r
                                                              float* __restrict__ sa) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
-  const int GU = G / U;  // U divides G
   const int used = off[E];
-  if (gid >= static_cast<int64_t>(used) * GU) return;  // a whole 16-lane set leaves together
-  const int64_t row = gid / GU;
-  if (row_token[row] < 0) return;  // padding row: a whole 16-lane set leaves together
-  const int g0 = static_cast<int>(gid - row * GU) * U;
-  const uint16_t* hr = h + row * ldh + g0 * 128 + sub * 8;
-  uint4 gv[U], uv[U];
+  const int64_t total = static_cast<int64_t>(used) * G;
+  if (gid >= total) return;  // a whole 16-lane group leaves together
+  const int64_t row = gid / G;
+  if (row_token[row] < 0) return;  // padding row: a whole 16-lane group leaves together
+  const int g = static_cast<int>(gid - row * G);
+  const uint16_t* hr = h + row * ldh + g * 128 + sub * 8;
+  const uint4 gv = *reinterpret_cast<const uint4*>(hr);
+  const uint4 uv = *reinterpret_cast<const uint4*>(hr + inter);
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t out[4];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    gv[u] = *reinterpret_cast<const uint4*>(hr + u * 128);
-    uv[u] = *reinterpret_cast<const uint4*>(hr + u * 128 + inter);
+  for (int i = 0; i < 4; ++i) {
+    const float g0 = bits_f32(gw[i] << 16), g1 = bits_f32(gw[i] & 0xffff0000u);
+    const float u0 = bits_f32(uw[i] << 16), u1 = bits_f32(uw[i] & 0xffff0000u);
+    const uint32_t p0 = bf16_rne(mul_rn(silu_ref(g0), u0));
+    const uint32_t p1 = bf16_rne(mul_rn(silu_ref(g1), u1));
+    out[i] = p0 | (p1 << 16);
   }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const uint32_t gw[4] = {gv[u].x, gv[u].y, gv[u].z, gv[u].w}, uw[4] = {uv[u].x, uv[u].y, uv[u].z, uv[u].w};
-    uint32_t out[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float g0f = bits_f32(gw[i] << 16), g1f = bits_f32(gw[i] & 0xffff0000u);
-      const float u0 = bits_f32(uw[i] << 16), u1 = bits_f32(uw[i] & 0xffff0000u);
-      const uint32_t p0 = bf16_rne(mul_rn(silu_ref(g0f), u0));
-      const uint32_t p1 = bf16_rne(mul_rn(silu_ref(g1f), u1));
-      out[i] = p0 | (p1 << 16);
-    }
-    float sc;
-    const uint2 codes = quant_group8(make_uint4(out[0], out[1], out[2], out[3]), true, HALF, &sc);
-    const int64_t slot = static_cast<int64_t>(g0 + u) * rows + row;
-    *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = codes;
-    if (sub == 0) sa[slot] = sc;
-  }
+  float s;
+  const uint2 codes = quant_group8(make_uint4(out[0], out[1], out[2], out[3]), true, HALF, &s);
+  const int64_t slot = static_cast<int64_t>(g) * rows + row;
+  *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = codes;
+  if (sub == 0) sa[slot] = s;
 }
 
 // ---- combine: y[t] = bf16(w_0 z_0 + w_1 z_1), 8 columns per thread -------------------
@@ -264,17 +255,12 @@ hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, cons
                                  const int32_t* row_token, int E, int rows, uint8_t* q, float* sa, bool half,
                                  hipStream_t stream) {
   const int G = inter / 128;
-  const bool four = G % 4 == 0;  // four groups per 16-lane set where they divide the row
-  const int64_t sets = static_cast<int64_t>(rows) * (four ? G / 4 : G);
-  const int blocks = static_cast<int>((sets + 15) / 16);
-#define GK_SMQ(H, U) \
-  silu_mul_quant_kernel<H, U><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa)
-  if (half) {
-    if (four) GK_SMQ(true, 4); else GK_SMQ(true, 1);
-  } else {
-    if (four) GK_SMQ(false, 4); else GK_SMQ(false, 1);
-  }
-#undef GK_SMQ
+  const int64_t groups = static_cast<int64_t>(rows) * G;
+  const int blocks = static_cast<int>((groups + 15) / 16);
+  if (half)
+    silu_mul_quant_kernel<true><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa);
+  else
+    silu_mul_quant_kernel<false><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa);
   return hipGetLastError();
 }
 
