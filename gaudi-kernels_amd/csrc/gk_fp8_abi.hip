@@ -342,6 +342,22 @@ gk_status gk_fp8_pack_weight(const void* w, int64_t n, int64_t k, void* packed, 
                                          static_cast<uint8_t*>(packed), static_cast<hipStream_t>(stream)));
 }
 
+gk_status gk_fp8_pack_experts(const void* w, int64_t e, int64_t n, int64_t k, void* packed, size_t packed_bytes,
+                              void* stream) {
+  if (!w || !packed) return GK_INVALID_ARGUMENT;
+  if (e < 1 || e > gk::kMoeMaxExperts) return GK_INCOMPATIBLE_INPUT_SIZE;
+  size_t per = 0;
+  gk_status st = gk_fp8_packed_weight_bytes(n, k, &per);
+  if (st != GK_SUCCESS) return st;
+  if (packed_bytes / per < static_cast<size_t>(e)) return GK_INSUFFICIENT_BUFFER;
+  if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(packed)) & 15) return GK_INCOMPATIBLE_DATA_TYPE;
+  st = current_device_ok();
+  if (st != GK_SUCCESS) return st;
+  return from_hip(gk::launch_pack_experts(static_cast<const uint8_t*>(w), static_cast<int>(e), static_cast<int>(n),
+                                          static_cast<int>(k), static_cast<uint8_t*>(packed),
+                                          static_cast<hipStream_t>(stream)));
+}
+
 gk_status gk_fp8_block_gemm_plan(int64_t m, int64_t n, int64_t k, uint32_t flags, const void* w, int* variant,
                                  int64_t* m_pad, size_t* workspace_bytes) {
   Plan p;

@@ -205,17 +205,39 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
 // group g), piece (h, l) = ((o / 64) % 2, o % 64) <- bytes [128 g + 32 (l/16)
 // + 16 h, +16) of row 16 t + l%16; rows >= N give zeros.  The writes are
 // contiguous; each wave's reads cover 16 rows x 64 bytes.
+//
+// Block order: tile-major (PANELS = false: b = t G + g, launch_pack_weight)
+// or, for expert weights, panel-major (launch_pack_experts): tiles in panels
+// of 16 (256 rows); panel p's blocks start at p 16 G, group by group, each
+// group's nbp = min(16, T - 16 p) tiles side by side (b = 16 G p + g nbp +
+// t % 16).  Both orders hold the same blocks in the same T G 2 KB.  Expert e
+// starts at e T G 2 KB (grid over all experts).
+template <bool PANELS>
 __global__ __launch_bounds__(256) void pack_weight_kernel(const uint8_t* __restrict__ w, int N, int K, int G,
-                                                          uint8_t* __restrict__ out, int64_t pieces) {
+                                                          uint8_t* __restrict__ out, int64_t pieces,
+                                                          int64_t per_expert) {
+  const int T = (N + 15) >> 4;
   for (int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; o < pieces;
        o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t b = o >> 7;
-    const int h = static_cast<int>((o >> 6) & 1), l = static_cast<int>(o & 63);
-    const int t = static_cast<int>(b / G), g = static_cast<int>(b - static_cast<int64_t>(t) * G);
+    const int64_t e = o / per_expert, oe = o - e * per_expert;
+    const int64_t b = oe >> 7;
+    const int h = static_cast<int>((oe >> 6) & 1), l = static_cast<int>(oe & 63);
+    int t, g;
+    if (PANELS) {
+      const int p = static_cast<int>(b / (16 * G));
+      const int r = static_cast<int>(b - static_cast<int64_t>(p) * 16 * G);
+      const int nbp = min(16, T - 16 * p);
+      g = r / nbp;
+      t = 16 * p + (r - g * nbp);
+    } else {
+      t = static_cast<int>(b / G);
+      g = static_cast<int>(b - static_cast<int64_t>(t) * G);
+    }
     const int row = 16 * t + (l & 15);
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (row < N)
-      v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(row) * K + 128 * g + 32 * (l >> 4) + 16 * h);
+      v = *reinterpret_cast<const uint4*>(w + (e * N + row) * static_cast<int64_t>(K) + 128 * g + 32 * (l >> 4) +
+                                          16 * h);
     *reinterpret_cast<uint4*>(out + o * 16) = v;
   }
 }
@@ -261,7 +283,14 @@ hipError_t launch_codec(bool forward, const uint8_t* src, uint8_t* dst, int64_t 
 hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, hipStream_t stream) {
   if (N < 1 || K < 128 || K % 128 != 0) return hipErrorInvalidValue;
   const int64_t pieces = packed_weight_bytes(N, K) / 16;
-  pack_weight_kernel<<<codec_grid(pieces), 256, 0, stream>>>(w, N, K, K / 128, packed, pieces);
+  pack_weight_kernel<false><<<codec_grid(pieces), 256, 0, stream>>>(w, N, K, K / 128, packed, pieces, pieces);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_experts(const uint8_t* w, int E, int N, int K, uint8_t* packed, hipStream_t stream) {
+  if (E < 1 || N < 1 || K < 128 || K % 128 != 0) return hipErrorInvalidValue;
+  const int64_t per = packed_weight_bytes(N, K) / 16;
+  pack_weight_kernel<true><<<codec_grid(per * E), 256, 0, stream>>>(w, N, K, K / 128, packed, per * E, per);
   return hipGetLastError();
 }
 

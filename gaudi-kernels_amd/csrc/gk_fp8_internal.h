@@ -137,6 +137,7 @@ __device__ inline float abs_max8(float m, uint4 v) {
 
 inline int64_t packed_weight_bytes(int64_t N, int64_t K) { return (N + 15) / 16 * 16 * K; }
 hipError_t launch_pack_weight(const uint8_t* w, int N, int K, uint8_t* packed, hipStream_t stream);
+hipError_t launch_pack_experts(const uint8_t* w, int E, int N, int K, uint8_t* packed, hipStream_t stream);
 
 // packed: the decode fragment layout (Mpad = 16, 32 or 64): the 2 KB block
 // (group g, token tile t) at (g * Mpad/16 + t) * 2048 holds, in its 16-byte

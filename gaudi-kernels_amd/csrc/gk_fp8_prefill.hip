@@ -60,10 +60,11 @@ constexpr int kLdsBytes = (kWStages + kAStages) * kTile;  // 160 KB: all of the 
 // are w + e * w_stride and scales sw + e * sw_stride.  Tiles past
 // group_off[n_groups] exit at once.
 //
-// Live rows: a wave skips the MFMAs, fragment reads and stores of its 32-row
-// blocks that lie past the tile's live rows (rows >= M, or past the expert's
-// live rows): their outputs are never read.  The other wave of the SIMD then
-// has the matrix core to itself.
+// Live rows: a wave skips the stores of its 16-row blocks that lie past the
+// tile's live rows (rows >= M, or past the expert's live rows), whose outputs
+// are never read; in the grouped form it skips their MFMAs and fragment reads
+// too, and the two waves of a SIMD take alternate blocks, so both keep a
+// share of the live rows.
 //
 // fp32 output (yp != nullptr): the tile stores fp32 sums to yp[part][m][n]
 // (row stride ldyp, plane stride M * ldyp) instead of bf16 y (no bias).  K
@@ -84,7 +85,11 @@ constexpr int kLdsBytes = (kWStages + kAStages) * kTile;  // 160 KB: all of the 
 // block (r / 16, g).  The weight tile is kept in LDS in that packed order, so
 // each loader instruction copies 1 KB of contiguous global memory (wave w:
 // blocks 2w and 2w + 1), and a fragment's two chunks (fc, fc + 1) are the
-// pieces h = 0, 1 of one lane slot, 1024 bytes apart.
+// pieces h = 0, 1 of one lane slot, 1024 bytes apart.  The grouped form reads
+// the experts' panel-major order (launch_pack_experts): the same 2 KB blocks,
+// each 256-row panel's blocks of one group side by side, so a step's weight
+// tile is one contiguous run (measured on MI355X, config 5 gate_up: 259 ->
+// 243 us; in the tile-major order a step reads 16 pieces 64 KB apart).
 //
 // NA: 16-row weight blocks per wave; the tile is 64 NA weight rows (256, or
 // 192 for the narrow tiles that fill the last round of a large GEMM).  A
@@ -108,6 +113,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
   const int wn = wave & 3, wm = wave >> 2;
   constexpr int BN = 64 * NA;  // weight rows of the tile
+  static_assert(!(GROUPED && WPACK) || NA == 4, "panel-major experts come in 256-row panels");
   const int tiles_m = Mpad / kBM;
   const int tiles = tiles_m * ((N + BN - 1) / BN);
   const int part = static_cast<int>(blockIdx.x) / tiles, bid = static_cast<int>(blockIdx.x) % tiles;
@@ -171,7 +177,9 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   // Exactly NA weight and four activation load instructions a step: the
   // step's wait counts on it.  Packed weights: wave w copies the 1 KB pieces
   // p = NA w + i of the tile (block p / 2, half p % 2; blocks past the last
-  // re-read the last one).
+  // re-read the last one).  Panel-major (GROUPED): block b of group g sits at
+  // (g nbp + b) 2 KB in the panel, nbp = the panel's blocks.
+  const int nbp = min(16, nblk + 1);
   auto issue_w_one = [&](int g, int ws, int i) {
     uint8_t* base = smem + ws * kTile + wave * 8 * NA * 128;
     uint32_t vo, so;
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
       const int p = NA * wave + i;
       const int blk = min(p >> 1, nblk);
       vo = lane16;
-      so = static_cast<uint32_t>((blk * gs + g) * 2048 + (p & 1) * 1024);
+      so = static_cast<uint32_t>((GROUPED ? g * nbp + blk : blk * gs + g) * 2048 + (p & 1) * 1024);
     } else {
       vo = aoff[i];
       so = static_cast<uint32_t>(g) * 128u;
@@ -232,9 +240,17 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   const uint32_t arow = WPACK ? static_cast<uint32_t>(wn * NA * 2048 + 16 * lane)
                               : static_cast<uint32_t>((wn * 16 * NA + fr) * 128);
   const uint32_t ya0 = WPACK ? 0u : xo0, ya1 = WPACK ? 1024u : xo1;
-  // activation block j of this wave: tokens wm*128 + 16 j
-  const uint32_t brow = static_cast<uint32_t>(kWStages * kTile + (wm * 128 + fr) * 128);
-  const float* sap = sa + (m0 + wm * 128 + fr);  // + 16 j + g * Mpad  (m0 + 256 <= Mpad)
+  // activation block j of this wave: tile rows mw + kJS j.  Dense: the wave's
+  // own 128 rows (mw = 128 wm, kJS = 16).  Grouped: the two waves of a SIMD
+  // take alternate 16-row blocks (mw = 16 wm, kJS = 32), so an expert segment
+  // that ends inside the tile leaves both with about half of its live rows
+  // (a lone wave per SIMD hides none of its read and MFMA latency; measured on
+  // MI355X, config 5 gate_up with the loads taken out: 191 us).  Each output
+  // element's arithmetic is the same either way.
+  constexpr int kJS = GROUPED ? 32 : 16, kJB = kJS * 128;  // block stride in rows and in LDS bytes
+  const int mw = GROUPED ? 16 * wm : 128 * wm;
+  const uint32_t brow = static_cast<uint32_t>(kWStages * kTile + (mw + fr) * 128);
+  const float* sap = sa + (m0 + mw + fr);  // + kJS j + g * Mpad  (m0 + 256 <= Mpad)
   // weight scale rows of the wave's blocks (one for NA = 4: 64 rows at a multiple of 64)
   constexpr int kScales = NA == 4 ? 1 : NA;
   const float* swp[kScales];
@@ -242,10 +258,10 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   for (int i = 0; i < kScales; ++i)
     swp[i] = sw + static_cast<int64_t>(min(n0 + wn * 16 * NA + 16 * i, N - 1) >> 7) * gs;
   float* ypp = yp ? yp + static_cast<int64_t>(part) * M * ldyp : nullptr;
-  // 16-token blocks of this wave's 128 rows that hold live rows (wave-uniform)
-  const int jl = min(8, max(0, (live - wm * 128 + 15) / 16));
+  // the wave's blocks that hold live rows: j < jl (wave-uniform)
+  const int jl = min(8, max(0, (live - mw + kJS - 1) / kJS));
 
-  // Accumulator acc[i][j] register r is output (m0 + wm*128 + 16 j + fr,
+  // Accumulator acc[i][j] register r is output (m0 + mw + kJS j + fr,
   // n0 + wn*16*NA + 16 i + 4 fq + r).  With accum the sums start from the fp32
   // partial in yp, so K ranges accumulated over several calls give the bits
   // of one call over their union.
@@ -257,7 +273,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   if (accum) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int m = m0 + wm * 128 + j * 16 + fr;
+      const int m = m0 + mw + j * kJS + fr;
       if (j >= jl || m >= M) continue;
 #pragma unroll
       for (int i = 0; i < NA; ++i) {
@@ -281,7 +297,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   auto load_sav = [&](int g) {
     if (!CH) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sv[j] = sap[j * 16 + static_cast<int64_t>(g) * Mpad];
+      for (int j = 0; j < 8; ++j) sv[j] = sap[j * kJS + static_cast<int64_t>(g) * Mpad];
     }
   };
   // One token block: NA MFMAs on the weight fragments.
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
       v8i b[kNB];
       unroll_each([&](auto uc) {
         constexpr int u = decltype(uc)::value;
-        b[u] = lds_frag_at<u * 2048>(B0, B1);
+        b[u] = lds_frag_at<u * kJB>(B0, B1);
       }, std::make_integer_sequence<int, kNB - 1>{});
       v4f t[2][NA];
       unroll_each([&](auto jc) {
@@ -365,7 +381,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
         }
         // block j + kNB - 1's read goes out; then block j's fragment must be in,
         // with the reads of blocks j + 1 .. min(7, j + kNB - 1) still in flight
-        if (j + kNB - 1 < 8) b[(j + kNB - 1) % kNB] = lds_frag_at<(j + kNB - 1) * 2048>(B0, B1);
+        if (j + kNB - 1 < 8) b[(j + kNB - 1) % kNB] = lds_frag_at<(j + kNB - 1) * kJB>(B0, B1);
         constexpr int later = (kNB - 1 < 7 - j) ? kNB - 1 : 7 - j;
         if (j == 0) {  // ... and the weight fragments, read before block 0's
           asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a[0]), "+v"(a[NA - 1]), "+v"(b[0]) : "n"(2 * later));
@@ -408,7 +424,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (j < jl) {
-        const int m = m0 + wm * 128 + j * 16 + fr;
+        const int m = m0 + mw + j * kJS + fr;
         if (m < M) {
           const float sam = sa[m];
           uint16_t* row = y + static_cast<int64_t>(m) * ldy;
@@ -428,7 +444,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (j < jl) {
-        const int m = m0 + wm * 128 + j * 16 + fr;
+        const int m = m0 + mw + j * kJS + fr;
         if (m >= M) continue;
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
@@ -452,7 +468,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
     if (j < jl) {
 #pragma unroll
       for (int i = 0; i < NA; ++i)
-        store_tile(y, ldy, bias, M, N, m0 + wm * 128 + j * 16 + fr, n0 + wn * 16 * NA + i * 16 + 4 * fq, acc[i][j]);
+        store_tile(y, ldy, bias, M, N, m0 + mw + j * kJS + fr, n0 + wn * 16 * NA + i * 16 + 4 * fq, acc[i][j]);
     }
   }
 }

@@ -68,6 +68,7 @@ SIGNATURES = {
     "gk_fp8_codec_half_to_ocp": (_c_int, [_c_vp, _c_vp, _c_i64, _fp, _fp, _c_i64, _c_vp, _c_size, _c_vp]),
     "gk_fp8_packed_weight_bytes": (_c_int, [_c_i64, _c_i64, ctypes.POINTER(_c_size)]),
     "gk_fp8_pack_weight": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_size, _c_vp]),
+    "gk_fp8_pack_experts": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_size, _c_vp]),
     "gk_fp8_act_quant_bf16": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _fp, _c_i64, _c_u32, _c_vp]),
     "gk_fp8_block_gemm_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_u32, _c_vp, ctypes.POINTER(_c_int),
                                         ctypes.POINTER(_c_i64), ctypes.POINTER(_c_size)]),

@@ -170,7 +170,7 @@ def pack_weight(weight):
 
 
 class PackedExperts:
-    """Expert weights [E, n, k] packed one expert after the other (pack_experts) for moe_block_fp8."""
+    """Expert weights [E, n, k] in the panel-major packed order (pack_experts) for moe_block_fp8."""
 
     def __init__(self, data, e, n, k):
         self.data, self.e, self.n, self.k = data, e, n, k
@@ -186,18 +186,15 @@ class PackedExperts:
 
 def pack_experts(weights):
     """Row-major E4M3 expert codes [E, N, K] (K % 128 == 0) on the GPU -> PackedExperts (asynchronous):
-    expert e packed by gk_fp8_pack_weight at byte e * packed_weight_bytes(N, K)."""
+    gk_fp8_pack_experts, expert e at byte e * packed_weight_bytes(N, K), each 256-row panel's blocks of one
+    128-K group side by side."""
     device = require_device(weights.device)
     if weights.dtype not in (torch.float8_e4m3fn, torch.uint8) or weights.ndim != 3 or not weights.is_contiguous():
         raise ValueError("expected contiguous E4M3 expert weights [E, N, K]")
     e, n, k = weights.shape
-    per = packed_weight_bytes(n, k)
-    data = torch.empty(e * per, dtype=torch.uint8, device=device)
-    lib = nat.load()
-    src = _u8(weights)
-    for i in range(e):
-        nat.check("gk_fp8_pack_weight",
-                  lib.gk_fp8_pack_weight(_ptr(src[i]), n, k, _ptr(data[i * per:]), per, _stream(device)))
+    data = torch.empty(e * packed_weight_bytes(n, k), dtype=torch.uint8, device=device)
+    nat.check("gk_fp8_pack_experts",
+              nat.load().gk_fp8_pack_experts(_ptr(_u8(weights)), e, n, k, _ptr(data), data.numel(), _stream(device)))
     return PackedExperts(data, e, n, k)
 
 

@@ -124,6 +124,19 @@ gk_status gk_fp8_packed_weight_bytes(int64_t n, int64_t k, size_t* bytes);
 gk_status gk_fp8_pack_weight(const void* w, int64_t n, int64_t k, void* packed, size_t packed_bytes,
                              void* stream);
 
+/* Expert weights for the MoE layer (gk_fp8_moe_bf16 with GK_FLAG_WEIGHT_PACKED):
+ * w E4M3 codes [e, n, k] (contiguous) -> packed, expert i at byte
+ * i * gk_fp8_packed_weight_bytes(n, k) (packed_bytes >= e times that, 16-byte
+ * aligned).  The same 2 KB blocks as gk_fp8_pack_weight in panel-major order:
+ * tiles in panels of 16 (256 rows), panel p's blocks starting at block
+ * 16 * G * p, group by group, each group's nbp = min(16, T - 16 p) tiles side
+ * by side (block 16 G p + g nbp + t % 16, T = ceil(n/16), G = k/128), so the
+ * grouped GEMM reads each step's 256-row weight tile as one contiguous run.
+ * No reference function: the reference has no MoE code (pack_weight's
+ * fp8_codec.py:19 note applies).  Stream-ordered, no synchronization. */
+gk_status gk_fp8_pack_experts(const void* w, int64_t e, int64_t n, int64_t k, void* packed, size_t packed_bytes,
+                              void* stream);
+
 /* ---- activation quantization ------------------------------------------------ */
 
 /* Per-row 1x128 E4M3 quantization with the oracle's scale rule
@@ -396,9 +409,8 @@ gk_status gk_fp8_rms_norm_quant_bf16(const void* x, const void* residual, int64_
  * scales fp32 [E, 2I/128, H/128], w_dn E4M3 [E, H, I] with scales fp32
  * [E, H/128, I/128], y bf16 [T, H] (row stride ldy).  H and I multiples of
  * 128, E <= 256; x, y, weights 16-byte aligned with ldx, ldy multiples of 8.
- * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_WEIGHT_PACKED: both w_gu and w_dn hold
- * each expert's weights packed by gk_fp8_pack_weight, expert e at byte
- * e * gk_fp8_packed_weight_bytes(n, k) (the results are bit-identical). */
+ * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_WEIGHT_PACKED: w_gu and w_dn are
+ * gk_fp8_pack_experts outputs (the results are bit-identical). */
 
 /* Padded row count of the expert-sorted layout: an upper bound of
  * sum_e round_up(count_e, 256), i.e. round_up(T*top_k + 255*E, 256). */

@@ -113,10 +113,11 @@ def test_moe_small_full_parity(t, h, inter, e, k, native_half):
     assert max_rel <= block_fp8.MAX_REL_TOL and mean_rel <= block_fp8.MEAN_REL_TOL, (max_rel, mean_rel)
 
 
+@pytest.mark.parametrize("t,h,inter,e,k", [(300, 512, 384, 4, 2), (200, 384, 256, 3, 2)])
 @pytest.mark.parametrize("native_half", [False, True])
-def test_moe_packed_experts_bit_identical(native_half):
-    """Expert weights packed at load time (pack_experts) give the row-major layer's bits."""
-    t, h, inter, e, k = 300, 512, 384, 4, 2
+def test_moe_packed_experts_bit_identical(t, h, inter, e, k, native_half):
+    """Expert weights packed at load time (pack_experts) give the row-major layer's bits; H = 384 leaves
+    the down GEMM a last weight panel of 8 tiles."""
     gen = torch.Generator().manual_seed(41)
     x = synth.activations(t, h, seed=42).cuda()
     logits = torch.randn(t, e, generator=gen).cuda()

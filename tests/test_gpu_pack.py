@@ -31,6 +31,15 @@ def test_pack_bytes(n, k):
     assert np.array_equal(p.data.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("e,n,k", [(1, 4096, 14336), (3, 264, 256), (2, 40, 384), (8, 768, 512), (2, 520, 128)])
+def test_pack_experts_bytes(e, n, k):
+    """gk_fp8_pack_experts (panel-major, all experts in one launch) equals oracle/pack.py."""
+    w = torch.randint(0, 256, (e, n, k), dtype=torch.uint8, generator=torch.Generator().manual_seed(e * n + k))
+    p = ops.pack_experts(w.cuda())
+    assert p.shape == (e, n, k)
+    assert np.array_equal(p.data.cpu().numpy(), pack.pack_experts(w.numpy()))
+
+
 CASES = [(1, 6144, 4096), (5, 1000, 256), (16, 28672, 4096), (16, 4096, 14336), (17, 264, 1024),
          (40, 7168, 7168), (64, 6144, 4096), (33, 28672, 512), (100, 1000, 512), (300, 6144, 4096),
          (600, 520, 384)]
@@ -82,3 +91,11 @@ def test_packed_rejections():
     small = ops.PackedWeight(p.data[:1024], 256, 256)
     with pytest.raises(ValueError):
         ops.block_fp8_gemm(x, small, s)
+    with pytest.raises(nat.GkError):
+        ops.pack_experts(torch.zeros(2, 16, 200, dtype=torch.uint8, device="cuda"))
+    lib, buf = nat.load(), torch.empty(2 * 16 * 128, dtype=torch.uint8, device="cuda")
+    src = torch.zeros(2, 16, 128, dtype=torch.uint8, device="cuda")
+    assert lib.gk_fp8_pack_experts(src.data_ptr(), 2, 16, 128, buf.data_ptr(), buf.numel() - 1, None) \
+        == nat.GK_INSUFFICIENT_BUFFER
+    assert lib.gk_fp8_pack_experts(src.data_ptr(), 0, 16, 128, buf.data_ptr(), buf.numel(), None) \
+        == nat.GK_INCOMPATIBLE_INPUT_SIZE
