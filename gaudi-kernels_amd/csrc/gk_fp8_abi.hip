@@ -875,6 +875,8 @@ gk_status moe_rows(int64_t T, int64_t E, int top_k, int64_t* rows) {
 
 gk_status moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, MoeLayout* L) {
   if (H < 128 || I < 128 || H % 128 || I % 128 || H > kMaxDim || I > kMaxDim / 2) return GK_INCOMPATIBLE_INPUT_SIZE;
+  // the gather and SiLU quantizers take one grid row (gridDim.y <= 65535) per 128-column group
+  if (H / 128 > 65535 || I / 128 > 65535) return GK_INCOMPATIBLE_INPUT_SIZE;
   gk_status st = moe_rows(T, E, top_k, &L->rows);
   if (st != GK_SUCCESS) return st;
   // the grouped GEMMs address the gathered activations with 32-bit offsets
@@ -972,8 +974,8 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   uint8_t* q1 = ws + L.q1;
   float* sa1 = reinterpret_cast<float*>(ws + L.sa1);
-  e = gk::launch_act_quant_rows(static_cast<const uint16_t*>(x), ldx, static_cast<int>(H), r.row_token, R, q1, sa1,
-                                half, s);
+  e = gk::launch_act_quant_rows(static_cast<const uint16_t*>(x), ldx, static_cast<int>(H), r.row_of,
+                                static_cast<int>(T), top_k, R, q1, sa1, half, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   uint16_t* hpre = reinterpret_cast<uint16_t*>(ws + L.hpre);
   gk::GemmArgs a{};
@@ -984,7 +986,7 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   uint8_t* q2 = ws + L.q2;
   float* sa2 = reinterpret_cast<float*>(ws + L.sa2);
-  e = gk::launch_silu_mul_quant(hpre, 2 * I, static_cast<int>(I), r.off, r.row_token, static_cast<int>(E), R, q2, sa2,
+  e = gk::launch_silu_mul_quant(hpre, 2 * I, static_cast<int>(I), r.row_of, static_cast<int>(T) * top_k, R, q2, sa2,
                                 half, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   float* z = reinterpret_cast<float*>(ws + L.z);

@@ -265,11 +265,10 @@ constexpr int kMoeMaxExperts = 256;
 
 hipError_t launch_moe_route(const float* logits, int T, int E, int64_t ld_logits, int top_k, int rows_max,
                             const MoeRouting& r, hipStream_t stream);
-hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_token, int rows,
-                                 uint8_t* q, float* sa, bool half, hipStream_t stream);
-hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off,
-                                 const int32_t* row_token, int E, int rows, uint8_t* q, float* sa, bool half,
-                                 hipStream_t stream);
+hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_of, int T, int top_k,
+                                 int rows, uint8_t* q, float* sa, bool half, hipStream_t stream);
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* row_of, int slots,
+                                 int rows, uint8_t* q, float* sa, bool half, hipStream_t stream);
 // z: kparts fp32 planes [kparts][rows][H] of the down GEMM; y[t] = bf16(sum_k w_k bf16(sum_p z_p[row])).
 hipError_t launch_moe_combine(const float* z, int kparts, int64_t plane, int H, const int32_t* row_of,
                               const float* wts, int T, int top_k, uint16_t* y, int64_t ldy, hipStream_t stream);

@@ -101,10 +101,13 @@ __host__ __device__ inline float add_rn(float a, float b) {
 // passes through; g = +inf gives NaN there (its Newton-refined quotient
 // computes -inf + inf), and so here.  The quotient is the IEEE one.
 __host__ __device__ inline float silu_ref(float g) {
-  if (g != g) return g;
-  if (g <= -88.0f) return 0.0f;
-  if (g == __builtin_huge_valf()) return __builtin_nanf("");
-  return g / (1.0f + expf(-g));
+  // The quotient is evaluated for every g and the special cases are selected
+  // afterwards (same values as early returns, but no branches, so the GPU
+  // overlaps the exp and division latencies of consecutive elements).
+  const float q = g / (1.0f + expf(-g));
+  float r = g <= -88.0f ? 0.0f : q;
+  r = g == __builtin_huge_valf() ? __builtin_nanf("") : r;
+  return g != g ? g : r;
 }
 
 // GELU of the reference's gk_gelu_and_mul_bf16_v1 (csrc/tpc/generic_dense/

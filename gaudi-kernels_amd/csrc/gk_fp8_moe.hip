@@ -9,7 +9,8 @@
 //   * rows: one row per (token, slot), ordered by expert then token; each
 //     expert's segment starts at a multiple of kMoeRowAlign (256) so a GEMM
 //     row tile never spans two experts; padding rows carry no token and are
-//     quantized as zeros;
+//     never written (each GEMM output row depends on its own input row only,
+//     and no later stage reads a padding row's outputs);
 //   * act: h = bf16(silu(g) * u) in fp32 -- the reference's fused
 //     SiLU-and-mul (csrc/tpc/generic_dense/silu_and_mul_bf16.c:4-15), whose
 //     only rounding is the final product -- followed here by the same 1x128
@@ -129,61 +130,55 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
   }
 }
 
-// ---- gather + quantize rows: like act_quant_kernel, row r reads token row_token[r]
+// ---- gather + quantize rows: token t's groups, quantized once, go to the rows
+// row_of[t * top_k + s] of its k slots (padding rows are not written: their
+// GEMM outputs are never read).
 template <bool HALF>
-__global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int K,
-                                                             int G, const int32_t* __restrict__ row_token,
+__global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             const int32_t* __restrict__ row_of, int T, int top_k,
                                                              int rows, uint8_t* __restrict__ q,
                                                              float* __restrict__ sa) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  const int64_t total = static_cast<int64_t>(rows) * G;
-  const bool active = gid < total;
-  const int64_t row = active ? gid / G : 0;
-  const int g = active ? static_cast<int>(gid - row * G) : 0;
-  const int tok = active ? row_token[row] : -1;
-  const bool live = tok >= 0;
-  uint4 raw = make_uint4(0u, 0u, 0u, 0u);
-  if (live) raw = *reinterpret_cast<const uint4*>(x + tok * ldx + g * 128 + sub * 8);
+  // grid: x = 16 tokens per block, y = group (no division for the indices)
+  const int t = static_cast<int>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const int g = static_cast<int>(blockIdx.y), sub = threadIdx.x & 15;
+  if (t >= T) return;  // a whole 16-lane group leaves together
+  const uint4 raw = *reinterpret_cast<const uint4*>(x + t * ldx + g * 128 + sub * 8);
   float s;
-  const uint2 codes = quant_group8(raw, live, HALF, &s);
-  if (active) {
-    const int64_t slot = static_cast<int64_t>(g) * rows + row;
-    *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = live ? codes : make_uint2(0u, 0u);
-    if (sub == 0) sa[slot] = live ? s : 0.0f;
+  const uint2 codes = quant_group8(raw, true, HALF, &s);
+  for (int k = 0; k < top_k; ++k) {
+    const int64_t slot = static_cast<int64_t>(g) * rows + row_of[t * top_k + k];
+    *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = codes;
+    if (sub == 0) sa[slot] = s;
   }
 }
 
 // ---- fused SiLU-and-mul + 1x128 quantization ----------------------------------------
-// h: bf16 [rows, 2*inter] (gate | up); rows past off[E] and padding rows
-// (row_token < 0, whose gate_up outputs were never computed) are skipped.
+// h: bf16 [rows, 2*inter] (gate | up); one 16-lane set per (routed slot,
+// group): row row_of[slot] (padding rows, whose gate_up outputs are not
+// defined, are never visited).
 // Lane: 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
 template <bool HALF>
 __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ h, int64_t ldh, int inter,
-                                                             int G, const int32_t* __restrict__ off,
-                                                             const int32_t* __restrict__ row_token, int E,
+                                                             const int32_t* __restrict__ row_of, int slots,
                                                              int rows, uint8_t* __restrict__ q,
                                                              float* __restrict__ sa) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15;
-  const int used = off[E];
-  const int64_t total = static_cast<int64_t>(used) * G;
-  if (gid >= total) return;  // a whole 16-lane group leaves together
-  const int64_t row = gid / G;
-  if (row_token[row] < 0) return;  // padding row: a whole 16-lane group leaves together
-  const int g = static_cast<int>(gid - row * G);
+  // grid: x = 16 slots per block, y = group (no division for the indices)
+  const int i = static_cast<int>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const int g = static_cast<int>(blockIdx.y), sub = threadIdx.x & 15;
+  if (i >= slots) return;  // a whole 16-lane group leaves together
+  const int64_t row = row_of[i];
   const uint16_t* hr = h + row * ldh + g * 128 + sub * 8;
   const uint4 gv = *reinterpret_cast<const uint4*>(hr);
   const uint4 uv = *reinterpret_cast<const uint4*>(hr + inter);
   const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
   uint32_t out[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float g0 = bits_f32(gw[i] << 16), g1 = bits_f32(gw[i] & 0xffff0000u);
-    const float u0 = bits_f32(uw[i] << 16), u1 = bits_f32(uw[i] & 0xffff0000u);
+  for (int j = 0; j < 4; ++j) {
+    const float g0 = bits_f32(gw[j] << 16), g1 = bits_f32(gw[j] & 0xffff0000u);
+    const float u0 = bits_f32(uw[j] << 16), u1 = bits_f32(uw[j] & 0xffff0000u);
     const uint32_t p0 = bf16_rne(mul_rn(silu_ref(g0), u0));
     const uint32_t p1 = bf16_rne(mul_rn(silu_ref(g1), u1));
-    out[i] = p0 | (p1 << 16);
+    out[j] = p0 | (p1 << 16);
   }
   float s;
   const uint2 codes = quant_group8(make_uint4(out[0], out[1], out[2], out[3]), true, HALF, &s);
@@ -239,28 +234,23 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int64_t ld_logits
   return hipGetLastError();
 }
 
-hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_token, int rows,
-                                 uint8_t* q, float* sa, bool half, hipStream_t stream) {
-  const int G = K / 128;
-  const int64_t groups = static_cast<int64_t>(rows) * G;
-  const int blocks = static_cast<int>((groups + 15) / 16);
+hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_of, int T, int top_k,
+                                 int rows, uint8_t* q, float* sa, bool half, hipStream_t stream) {
+  const dim3 grid((T + 15) / 16, K / 128);
   if (half)
-    act_quant_rows_kernel<true><<<blocks, 256, 0, stream>>>(x, ldx, K, G, row_token, rows, q, sa);
+    act_quant_rows_kernel<true><<<grid, 256, 0, stream>>>(x, ldx, row_of, T, top_k, rows, q, sa);
   else
-    act_quant_rows_kernel<false><<<blocks, 256, 0, stream>>>(x, ldx, K, G, row_token, rows, q, sa);
+    act_quant_rows_kernel<false><<<grid, 256, 0, stream>>>(x, ldx, row_of, T, top_k, rows, q, sa);
   return hipGetLastError();
 }
 
-hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* off,
-                                 const int32_t* row_token, int E, int rows, uint8_t* q, float* sa, bool half,
-                                 hipStream_t stream) {
-  const int G = inter / 128;
-  const int64_t groups = static_cast<int64_t>(rows) * G;
-  const int blocks = static_cast<int>((groups + 15) / 16);
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* row_of, int slots,
+                                 int rows, uint8_t* q, float* sa, bool half, hipStream_t stream) {
+  const dim3 grid((slots + 15) / 16, inter / 128);
   if (half)
-    silu_mul_quant_kernel<true><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa);
+    silu_mul_quant_kernel<true><<<grid, 256, 0, stream>>>(h, ldh, inter, row_of, slots, rows, q, sa);
   else
-    silu_mul_quant_kernel<false><<<blocks, 256, 0, stream>>>(h, ldh, inter, G, off, row_token, E, rows, q, sa);
+    silu_mul_quant_kernel<false><<<grid, 256, 0, stream>>>(h, ldh, inter, row_of, slots, rows, q, sa);
   return hipGetLastError();
 }
 

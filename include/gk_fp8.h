@@ -408,7 +408,7 @@ gk_status gk_fp8_rms_norm_quant_bf16(const void* x, const void* residual, int64_
  * ld_logits), w_gu E4M3 [E, 2I, H] (gate rows 0..I-1, up rows I..2I-1) with
  * scales fp32 [E, 2I/128, H/128], w_dn E4M3 [E, H, I] with scales fp32
  * [E, H/128, I/128], y bf16 [T, H] (row stride ldy).  H and I multiples of
- * 128, E <= 256; x, y, weights 16-byte aligned with ldx, ldy multiples of 8.
+ * 128 up to 65535 * 128, E <= 256; x, y, weights 16-byte aligned with ldx, ldy multiples of 8.
  * flags: GK_FLAG_NATIVE_HALF; GK_FLAG_WEIGHT_PACKED: w_gu and w_dn are
  * gk_fp8_pack_experts outputs (the results are bit-identical). */
 
