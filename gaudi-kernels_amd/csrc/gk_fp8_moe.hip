@@ -48,26 +48,46 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
   for (int i = tid; i < rows_max; i += kRouteThreads) r.row_token[i] = -1;
   __syncthreads();
 
-  for (int t = tid; t < T; t += kRouteThreads) {
+  // ids of the first kKeep tokens of each thread stay in registers for phase 3
+  // (no global write-then-read round trip); later tokens are read back from r.ids
+  constexpr int kKeep = 4;
+  int keep0[kKeep], keep1[kKeep];
+#pragma unroll
+  for (int i = 0; i < kKeep; ++i) keep0[i] = keep1[i] = -1;
+  for (int t = tid, it = 0; t < T; t += kRouteThreads, ++it) {
     const float* row = logits + static_cast<int64_t>(t) * ld;
-    int best0 = 0;
-    float v0 = row[0];
-    for (int e = 1; e < E; ++e) {
-      const float v = row[e];
-      if (v > v0) { v0 = v; best0 = e; }
+    // One pass in expert order, eight logits loaded at a time.  best0: the
+    // first expert holding the maximum (strictly greater wins); best1: the
+    // same over the other experts -- a new maximum hands its predecessor to
+    // best1, which is then the first holder of the best value among the rest.
+    int best0 = 0, best1 = -1;
+    float v0 = 0.0f, v1 = 0.0f;
+    for (int c = 0; c < E; c += 8) {
+      float lv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) lv[u] = c + u < E ? row[c + u] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = c + u;
+        if (e >= E) break;
+        const float v = lv[u];
+        if (e == 0) {
+          v0 = v;
+        } else if (v > v0) {
+          best1 = best0; v1 = v0;
+          best0 = e; v0 = v;
+        } else if (best1 < 0 || v > v1) {
+          best1 = e; v1 = v;
+        }
+      }
     }
     r.ids[t * top_k] = best0;
     atomicAdd(&counts[best0], 1);
+    int kept1 = -1;
     if (top_k == 2) {
-      int best1 = -1;
-      float v1 = 0.0f;
-      for (int e = 0; e < E; ++e) {
-        if (e == best0) continue;
-        const float v = row[e];
-        if (best1 < 0 || v > v1) { v1 = v; best1 = e; }
-      }
       r.ids[t * 2 + 1] = best1;
       atomicAdd(&counts[best1], 1);
+      kept1 = best1;
       // softmax over (v0, v1) with v0 >= v1: exp(0) = 1 and exp(v1 - v0), fp32
       const float e1 = expf(v1 - v0);
       const float s = 1.0f + e1;
@@ -76,6 +96,12 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
     } else {
       r.wts[t] = 1.0f;
     }
+#pragma unroll
+    for (int i = 0; i < kKeep; ++i)
+      if (it == i) {
+        keep0[i] = best0;
+        keep1[i] = kept1;
+      }
   }
   __syncthreads();
   if (tid == 0) {
@@ -92,11 +118,21 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float* _
   if (r.cnt)
     for (int e = tid; e < E; e += kRouteThreads) r.cnt[e] = counts[e];
 
-  for (int base = 0; base < T; base += kRouteThreads) {
+  for (int base = 0, it = 0; base < T; base += kRouteThreads, ++it) {
     const int t = base + tid;
     const bool live = t < T;
-    const int e0 = live ? r.ids[t * top_k] : -1;
-    const int e1 = (live && top_k == 2) ? r.ids[t * 2 + 1] : -1;
+    int e0 = -1, e1 = -1;
+    if (it < kKeep) {
+#pragma unroll
+      for (int i = 0; i < kKeep; ++i)
+        if (it == i) {
+          e0 = keep0[i];
+          e1 = keep1[i];
+        }
+    } else {
+      e0 = live ? r.ids[t * top_k] : -1;
+      e1 = (live && top_k == 2) ? r.ids[t * 2 + 1] : -1;
+    }
     const unsigned long long below_lane = (1ull << lane) - 1ull;
     int rank0 = 0, rank1 = 0;
     for (int e = 0; e < E; ++e) {  // a token picks an expert at most once
