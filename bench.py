@@ -206,11 +206,19 @@ def rocprof_summary(directory):
                   f"{min(v) / 1e3:.2f} |")
         print()
     counters = defaultdict(list)
+    copy = defaultdict(list)  # counter -> values of the calibration copies
     for path in sorted(glob.glob(os.path.join(directory, "**", "*_counter_collection.csv"), recursive=True)):
         agg = defaultdict(list)
+        copies = defaultdict(list)
         for r in csv.DictReader(open(path)):
             agg[(kernel_short_name(r["Kernel_Name"]), r["Grid_Size"], r["Counter_Name"])].append(
                 float(r["Counter_Value"]))
+            if r["Kernel_Name"] == "__amd_rocclr_copyBuffer":
+                copies[r["Counter_Name"]].append((int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+        # a --profile run starts with the three 256 MiB calibration copies (copy_calibration); later
+        # copies (input set-up) have other sizes
+        for ctr, v in copies.items():
+            copy[ctr] += [val for _, val in sorted(v)[:3]]
         print(f"### counters: {os.path.relpath(path, directory)}\n")
         print("| kernel | grid (threads) | counter | dispatches | median | min | max |")
         print("|---|---|---|---|---|---|---|")
@@ -218,12 +226,9 @@ def rocprof_summary(directory):
             print(f"| `{name}` | {grid} | {ctr} | {len(v)} | {med(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
             counters[(name, grid, ctr)] += v
         print()
-    # Traffic: the 256 MiB copy of bench.py (largest __amd_rocclr_copyBuffer dispatch) calibrates the
-    # counters; each gk decode GEMM dispatch shape of a `--only decode` run (config 2) gets a line.
-    copy = {}
-    for (n, g, c), v in counters.items():
-        if n == "__amd_rocclr_copyBuffer":
-            copy[c] = max(copy.get(c, 0.0), max(v))
+    # Traffic: the 256 MiB calibration copies (the first three __amd_rocclr_copyBuffer dispatches of each
+    # --profile run) calibrate the counters; each gk GEMM dispatch shape gets a line.
+    copy = {c: med(v) for c, v in copy.items()}
     copy_bytes = 256 << 20
     if "FETCH_SIZE" in copy and "WRITE_SIZE" in copy:
         fs, ws = copy_bytes / 1024 / copy["FETCH_SIZE"], copy_bytes / 1024 / copy["WRITE_SIZE"]
