@@ -48,9 +48,9 @@ MALL_ROTATE_BYTES = 512 << 20
 # (NW=8, R=2, U=4, bf16 activations read directly, WPACK, one token tile) -- each op of the step is one
 # launch of it.
 DECODE_KERNEL = "gk::gemm_decode_kernel<8,2,4,false,false,false,true,true,1>"
-# The prefill roofline kernel: the 256 x 256 LDS-tiled MFMA kernel on packed weights (config 4).
-# config 4 is two launches of this kernel (template argument NA = 4 on 4096 columns, 3 on the other 3072)
-PREFILL_KERNEL = "gk::gemm_prefill256_kernel<false,false,false,true,"
+# The prefill roofline kernel: the 256 x 256 LDS-tiled MFMA kernel on packed weights (config 4), launched as the
+# split kernel: one launch with 256-wide tiles on 4096 columns and 192-wide tiles on the other 3072.
+PREFILL_KERNEL = "gk::gemm_prefill256_split_kernel<false,true>"
 SIMD_NUM = 1024  # 256 CUs x 4 SIMDs (MI355X)
 
 
@@ -266,9 +266,9 @@ WORKLOAD_BY_GRID = {"98304": "config2", "114688": "config3_gate_up", "131072": "
 
 
 def workload_of(kernel, grid):
-    """Workload of a GEMM dispatch in a profile summary: by grid, except the config 4 prefill launches (both tile
-    widths run 256 workgroups of 512 threads, the grid of config 3's down-projection decode launch)."""
-    if "prefill256" in kernel and grid == "131072":
+    """Workload of a GEMM dispatch in a profile summary: by grid, except the config 4 prefill launch (the split
+    kernel, 512 workgroups of 512 threads)."""
+    if "prefill256_split" in kernel:
         return "config4"
     return WORKLOAD_BY_GRID.get(grid, "grid" + grid)
 
@@ -726,8 +726,8 @@ def main():
         result["roofline_prefill"] = {
             "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": measured_traffic(PREFILL_KERNEL, "config4"),
-            "kernel": f"{PREFILL_KERNEL}NA> (config 4: M=4096, N=K=7168, one op = two launches, NA=4 tiles on "
-                      "4096 columns and NA=3 on 3072; packed weights, activations quantized beforehand)",
+            "kernel": f"{PREFILL_KERNEL} (config 4: M=4096, N=K=7168, one launch: 256-wide tiles on 4096 "
+                      "columns and 192-wide on 3072; packed weights, activations quantized beforehand)",
             "flops_per_op": f, "avg_op_us": round(ms4k * 1e3, 2),
             "op_frac": round(f / (ms4 * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
             "counters": None if counters is None else {

@@ -95,19 +95,18 @@ constexpr int kLdsBytes = (kWStages + kAStages) * kTile;  // 160 KB: all of the 
 // 192 for the narrow tiles that fill the last round of a large GEMM).  A
 // 48-row wave can straddle two 128-row scale blocks, so NA = 3 takes one
 // weight scale per block.
-template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
-__global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
-                                                              const float* __restrict__ sa,
-                                                              const uint8_t* __restrict__ w,
-                                                              const float* __restrict__ sw,
-                                                              const float* __restrict__ bias,
-                                                              uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                              int K, int G, int Mpad,
-                                                              const int32_t* __restrict__ group_off,
-                                                              const int32_t* __restrict__ group_cnt, int n_groups,
-                                                              int64_t w_stride, int64_t sw_stride, int kparts,
-                                                              float* __restrict__ yp, int64_t ldq, int gs,
-                                                              int64_t ldyp, int accum) {
+// The workgroup body; `block` is the workgroup's index within its launch (or
+// within its column range of the split launch below).
+template <bool HALF, bool GROUPED, bool CH, bool WPACK, int NA>
+__device__ __forceinline__ void prefill256_body(int block, const uint8_t* __restrict__ qa,
+                                                const float* __restrict__ sa, const uint8_t* __restrict__ w,
+                                                const float* __restrict__ sw, const float* __restrict__ bias,
+                                                uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int G,
+                                                int Mpad, const int32_t* __restrict__ group_off,
+                                                const int32_t* __restrict__ group_cnt, int n_groups,
+                                                int64_t w_stride, int64_t sw_stride, int kparts,
+                                                float* __restrict__ yp, int64_t ldq, int gs, int64_t ldyp,
+                                                int accum) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
@@ -116,7 +115,7 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   static_assert(!(GROUPED && WPACK) || NA == 4, "panel-major experts come in 256-row panels");
   const int tiles_m = Mpad / kBM;
   const int tiles = tiles_m * ((N + BN - 1) / BN);
-  const int part = static_cast<int>(blockIdx.x) / tiles, bid = static_cast<int>(blockIdx.x) % tiles;
+  const int part = block / tiles, bid = block % tiles;
   // Dense: consecutive workgroups share the weight panel.  Grouped: they take
   // consecutive panels of one expert segment, whose activation tiles then stay
   // in L2 (measured on MI355X, config 5 MoE layer: 482 -> 456 us).
@@ -478,11 +477,51 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
   }
 }
 
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
+__global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
+                                                              const float* __restrict__ sa,
+                                                              const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ sw,
+                                                              const float* __restrict__ bias,
+                                                              uint16_t* __restrict__ y, int64_t ldy, int M, int N,
+                                                              int K, int G, int Mpad,
+                                                              const int32_t* __restrict__ group_off,
+                                                              const int32_t* __restrict__ group_cnt, int n_groups,
+                                                              int64_t w_stride, int64_t sw_stride, int kparts,
+                                                              float* __restrict__ yp, int64_t ldq, int gs,
+                                                              int64_t ldyp, int accum) {
+  prefill256_body<HALF, GROUPED, CH, WPACK, NA>(static_cast<int>(blockIdx.x), qa, sa, w, sw, bias, y, ldy, M, N, K,
+                                                G, Mpad, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts,
+                                                yp, ldq, gs, ldyp, accum);
+}
+
+// A dense GEMM in two column ranges, one launch: workgroups [0, split) take
+// 256-wide tiles of columns [0, wide) and the rest 192-wide tiles of [wide, N)
+// (weights, scales, bias and outputs of the second range passed offset, with
+// n2 = N - wide columns).  One launch instead of two: workgroups of the second
+// range start on the CUs as the first range's finish, with no launch gap and
+// no idle tail between the ranges.
+template <bool HALF, bool WPACK>
+__global__ __launch_bounds__(512) void gemm_prefill256_split_kernel(
+    int split, const uint8_t* __restrict__ qa, const float* __restrict__ sa, int64_t ldy, int M, int K, int G,
+    int Mpad, int gs, int64_t ldyp, int accum, const uint8_t* __restrict__ w1, const float* __restrict__ sw1,
+    const float* __restrict__ bias1, uint16_t* __restrict__ y1, float* __restrict__ yp1, int n1,
+    const uint8_t* __restrict__ w2, const float* __restrict__ sw2, const float* __restrict__ bias2,
+    uint16_t* __restrict__ y2, float* __restrict__ yp2, int n2) {
+  const int b = static_cast<int>(blockIdx.x);
+  if (b < split)
+    prefill256_body<HALF, false, false, WPACK, 4>(b, qa, sa, w1, sw1, bias1, y1, ldy, M, n1, K, G, Mpad, nullptr,
+                                                  nullptr, 0, 0, 0, 1, yp1, 0, gs, ldyp, accum);
+  else
+    prefill256_body<HALF, false, false, WPACK, 3>(b - split, qa, sa, w2, sw2, bias2, y2, ldy, M, n2, K, G, Mpad,
+                                                  nullptr, nullptr, 0, 0, 0, 1, yp2, 0, gs, ldyp, accum);
+}
+
 // The 160 KB of dynamic LDS is above the default limit: raise it once per device.
 constexpr int kMaxDevices = 64;
 
-std::once_flag g_lds_once[kMaxDevices][32];
-hipError_t g_lds_err[kMaxDevices][32];
+std::once_flag g_lds_once[kMaxDevices][36];
+hipError_t g_lds_err[kMaxDevices][36];
 
 template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
 hipError_t ensure_lds_limit() {
@@ -497,6 +536,36 @@ hipError_t ensure_lds_limit() {
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   });
   return g_lds_err[dev][slot];
+}
+
+template <bool HALF, bool WPACK>
+hipError_t ensure_lds_limit_split() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  constexpr int slot = 32 + (HALF ? 1 : 0) + (WPACK ? 2 : 0);
+  std::call_once(g_lds_once[dev][slot], [dev] {
+    g_lds_err[dev][slot] = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_prefill256_split_kernel<HALF, WPACK>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  });
+  return g_lds_err[dev][slot];
+}
+
+template <bool HALF, bool WPACK>
+hipError_t launch_split(const GemmArgs& a, int wide, hipStream_t stream) {
+  hipError_t e = ensure_lds_limit_split<HALF, WPACK>();
+  if (e != hipSuccess) return e;
+  const int tiles_m = a.Mpad / kBM, n2 = a.N - wide;
+  const int split = tiles_m * (wide / 256);
+  const unsigned blocks = static_cast<unsigned>(split + tiles_m * ((n2 + 191) / 192));
+  // Columns [wide, N): weight rows from `wide` (row-major: + wide * K bytes; packed:
+  // 16-row tiles of gs * 2048 = K * 16 bytes, the same offset), scale rows from wide / 128.
+  gemm_prefill256_split_kernel<HALF, WPACK><<<blocks, 512, kLdsBytes, stream>>>(
+      split, a.qa, a.sa, a.ldy, a.M, a.K, a.G, a.Mpad, a.gstride(), a.ldyp, a.accumulate ? 1 : 0, a.w, a.sw, a.bias,
+      a.y, a.yp, wide, a.w + static_cast<int64_t>(wide) * a.K, a.sw + static_cast<int64_t>(wide / 128) * a.gstride(),
+      a.bias ? a.bias + wide : nullptr, a.y ? a.y + wide : nullptr, a.yp ? a.yp + wide : nullptr, n2);
+  return hipGetLastError();
 }
 
 template <bool HALF, bool GROUPED, bool WPACK = false, int NA = 4>
@@ -577,29 +646,16 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
 }
 
 // Requires K % 128 == 0, 16-byte aligned weights, Mpad % 256 == 0 (qa/sa
-// padded with zero rows up to Mpad).  Large GEMMs may run as two launches
-// over column ranges (prefill_wide_columns); each output column is computed
-// by one workgroup either way, with the same per-element arithmetic.
+// padded with zero rows up to Mpad).  Large GEMMs may run in two column
+// ranges of different tile widths (prefill_wide_columns), in one launch; each
+// output column is computed by one workgroup either way, with the same
+// per-element arithmetic.
 hipError_t launch_gemm_prefill256(const GemmArgs& a, hipStream_t stream) {
   if (a.Mpad % kBM != 0 || !prefill256_fits(a)) return hipErrorInvalidValue;
   const int wide = prefill_wide_columns(a.Mpad, a.N, device_cus());
   if (wide >= a.N) return launch_dense<4>(a, stream);
-  hipError_t e = launch_dense<4>([&] {
-    GemmArgs w = a;
-    w.N = wide;
-    return w;
-  }(), stream);
-  if (e != hipSuccess) return e;
-  // Columns [wide, N): weight rows from `wide` (row-major: + wide * K bytes; packed:
-  // 16-row tiles of gs * 2048 = K * 16 bytes, the same offset), scale rows from wide / 128.
-  GemmArgs r = a;
-  r.N = a.N - wide;
-  r.w = a.w + static_cast<int64_t>(wide) * a.K;
-  r.sw = a.sw + static_cast<int64_t>(wide / 128) * a.gstride();
-  if (a.bias) r.bias = a.bias + wide;
-  if (a.y) r.y = a.y + wide;
-  if (a.yp) r.yp = a.yp + wide;
-  return launch_dense<3>(r, stream);
+  if (a.wpack) return a.half_w ? launch_split<true, true>(a, wide, stream) : launch_split<false, true>(a, wide, stream);
+  return a.half_w ? launch_split<true, false>(a, wide, stream) : launch_split<false, false>(a, wide, stream);
 }
 
 // Grouped form: a.Mpad = padded rows (multiple of 256), a.M = a.Mpad; weights
