@@ -105,10 +105,18 @@ def capture(fn, iters):
     return graph
 
 
-def time_graph(graph, iters_in_graph, replays=3):
-    """Average ms per captured call, HIP events on the replay stream (torch's current stream)."""
-    graph.replay()
-    torch.cuda.synchronize()
+def time_graph(graph, iters_in_graph, replays=3, warm_s=0.02):
+    """Average ms per captured call, HIP events on the replay stream (torch's current stream).
+
+    Untimed replays first, for at least `warm_s` seconds and three replays: a graph's first replays after
+    other work run slower (measured on MI355X: the config 4 op 241, 221, then 216 us; a decode graph's
+    first replays 1.3 and 0.2 us per step above its later ones), so the timed replays start steady."""
+    t_end = time.perf_counter() + warm_s
+    done = 0
+    while done < 3 or time.perf_counter() < t_end:
+        graph.replay()
+        torch.cuda.synchronize()
+        done += 1
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(replays):
