@@ -40,8 +40,8 @@ namespace gk {
 // so sixteen lanes read 256 contiguous bytes (the MFMA operand layout instead
 // puts 16 different rows in 16 consecutive lanes, which the memory pipeline
 // serves about 1.5-2x slower).  The tile goes through a wave-private 2 KB LDS
-// buffer -- chunk c of row r at slot c ^ ((r >> 1) & 7), bank-conflict free
-// for both the write and the fragment read -- into the MFMA layout.
+// buffer -- chunk c of row r at slot c ^ lds_key(r), bank-conflict free for
+// both the write and the fragment read -- into the MFMA layout.
 //
 // K permutation (A and B alike): lane (col, quad) holds bytes [32 quad,
 // 32 quad + 32) of the group.  Activations come in one of two layouts:
@@ -121,10 +121,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_decode_kernel(const uint8_t* __r
     }
   }
   constexpr int kWG = WPACK ? 2048 : 128;  // weight bytes from one group to the next
-  const uint32_t woff0 = lrow * 128 + ((lch ^ ((lrow >> 1) & 7)) << 4);
-  const uint32_t woff1 = (lrow + 8) * 128 + ((lch ^ (((lrow + 8) >> 1) & 7)) << 4);
-  const uint32_t roff0 = col * 128 + (((2 * quad) ^ ((col >> 1) & 7)) << 4);
-  const uint32_t roff1 = col * 128 + (((2 * quad + 1) ^ ((col >> 1) & 7)) << 4);
+  const uint32_t woff0 = lrow * 128 + ((lch ^ lds_key(lrow)) << 4);
+  const uint32_t woff1 = (lrow + 8) * 128 + ((lch ^ lds_key(lrow + 8)) << 4);
+  const uint32_t roff0 = col * 128 + (((2 * quad) ^ lds_key(col)) << 4);
+  const uint32_t roff1 = col * 128 + (((2 * quad + 1) ^ lds_key(col)) << 4);
   // Token tile t holds tokens 16 t .. 16 t + 15; tokens >= M read token M-1.
   // Decode fragment layout: (group g, token tile tt) is the 2 KB block
   // g * MT + tt; standard layout: row tok of group g at (g * 16 MT + tok) * 128.

@@ -16,8 +16,9 @@
 //     Step g waits only for its own tiles: the weights of step g+1 and the
 //     token scales stay in flight across its barrier.
 //   * LDS rows are 128 bytes with the 16-byte chunk c of row r stored at slot
-//     c ^ ((r >> 1) & 7): sixteen consecutive rows reading one chunk hit 16
-//     distinct 16-byte bank groups (measured: zero LDS bank conflicts).
+//     c ^ lds_key(r) (gk_fp8_lds.h): the fragment reads of any 16 and of any
+//     32 consecutive lanes hit distinct 16-byte slots of a 256- and a
+//     512-byte window.
 //   * Fragment reads are issued as inline-asm ds_read_b128 with explicit
 //     lgkmcnt waits tied to the fragment registers.  The compiler then does
 //     not treat them as reads that may alias the in-flight direct-to-LDS
@@ -141,9 +142,9 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   const int r0 = wave * 32 + lr, rw0 = wave * 8 * NA + lr;
   int lcs[4], lcw[NA];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ (((r0 + 8 * i) >> 1) & 7)) * 16;
+  for (int i = 0; i < 4; ++i) lcs[i] = (ls ^ lds_key(r0 + 8 * i)) * 16;
 #pragma unroll
-  for (int i = 0; i < NA; ++i) lcw[i] = (ls ^ (((rw0 + 8 * i) >> 1) & 7)) * 16;
+  for (int i = 0; i < NA; ++i) lcw[i] = (ls ^ lds_key(rw0 + 8 * i)) * 16;
   // Loader addresses: a wave-uniform base (scalar registers) plus a per-lane
   // 32-bit offset.  Packed weights need one lane offset (lane * 16) and the
   // group-major activations two (the chunk key of rows r0 + 8 i alternates with
@@ -154,7 +155,8 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   const int nmax = N - 1 - n0, mmax = M - 1 - m0;
   const int nblk = ((N + 15) >> 4) - 1 - (n0 >> 4);  // last 16-row block of the panel
   const uint32_t lane16 = static_cast<uint32_t>(lane) * 16u;
-  const uint32_t bl0 = lr * 128 + ((ls ^ (lr >> 1)) << 4), bl1 = lr * 128 + ((ls ^ (lr >> 1) ^ 4) << 4);
+  // rows r0 + 8 i (r0 = 32 wave + lr): key lds_key(lr) for even i, lds_key(lr) ^ 4 for odd i
+  const uint32_t bl0 = lr * 128 + ((ls ^ lds_key(lr)) << 4), bl1 = lr * 128 + ((ls ^ lds_key(lr) ^ 4) << 4);
   uint32_t aoff[NA], boff[4];
 #pragma unroll
   for (int i = 0; i < NA; ++i) aoff[i] = static_cast<uint32_t>(min(rw0 + 8 * i, nmax) * K + lcw[i]);
@@ -229,10 +231,10 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
 
   // Fragments (16x16x128 operand layout): lane -> row (lane & 15) of a
   // 16-row block, K bytes [32 (lane >> 4), +32) = chunks 2 (lane >> 4) + {0, 1}.
-  // Row-major tiles keep chunk c of row r at slot c ^ ((r >> 1) & 7); the
+  // Row-major tiles keep chunk c of row r at slot c ^ lds_key(r); the
   // packed weight tile holds each 16-row block as 2 KB in fragment order
   // (piece h of lane l at h * 1024 + 16 l).
-  const int fr = lane & 15, fq = lane >> 4, kf = (fr >> 1) & 7;
+  const int fr = lane & 15, fq = lane >> 4, kf = lds_key(fr);
   const uint32_t xo0 = static_cast<uint32_t>(((2 * fq) ^ kf) << 4), xo1 = static_cast<uint32_t>(((2 * fq + 1) ^ kf) << 4);
   const uint32_t lbase = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
   // weight block i of this wave: rows wn*16*NA + 16 i

@@ -8,6 +8,16 @@ namespace gk {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Chunk key of tile row r: the 16-byte chunk c of row r sits at slot
+// c ^ lds_key(r) of its 128-byte LDS row.  Bits 3, 1, 2 of r give bits 2, 1,
+// 0 of the key, so a fragment read (16 consecutive rows, chunk 2q + h for the
+// lanes of quad q) lands on distinct 16-byte slots both within each 16-lane
+// quarter over a 256-byte window and within each 32-lane half over a
+// 512-byte window: conflict-free on gfx950, which serves a 128-bit LDS read
+// 32 lanes at a time (measured: the (r >> 1) & 7 key, distinct only over 256
+// bytes, read as 64 bank-conflict cycles per wave-step of the 256 x 256 kernel).
+__host__ __device__ constexpr int lds_key(int r) { return ((r >> 1) & 4) | (r & 2) | ((r >> 2) & 1); }
+
 // 16-byte streaming load (weights are read once per call: non-temporal hint).
 __device__ inline uint4 load_stream16(const uint8_t* p) {
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
