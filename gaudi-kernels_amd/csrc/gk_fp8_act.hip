@@ -31,8 +31,7 @@ template <int ACT>
 __device__ inline uint32_t act_mul_pair(uint32_t g2, uint32_t u2) {
   const float g0 = bits_f32(g2 << 16), g1 = bits_f32(g2 & 0xffff0000u);
   const float u0 = bits_f32(u2 << 16), u1 = bits_f32(u2 & 0xffff0000u);
-  return static_cast<uint32_t>(bf16_rne(mul_rn(act_ref<ACT>(g0), u0))) |
-         (static_cast<uint32_t>(bf16_rne(mul_rn(act_ref<ACT>(g1), u1))) << 16);
+  return bf16x2_rne(mul_rn(act_ref<ACT>(g0), u0), mul_rn(act_ref<ACT>(g1), u1));
 }
 
 template <int ACT>

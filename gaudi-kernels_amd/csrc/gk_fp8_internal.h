@@ -13,6 +13,22 @@ namespace gk {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// bf16_rne(a) | bf16_rne(b) << 16 with gfx950's v_cvt_pk_bf16_f32: it rounds
+// to nearest even and keeps denormals, equal to bf16_rne for every non-NaN
+// float (all 2^32 inputs: gk_probe_bf16x2_check), but keeps NaN payloads, so
+// NaN inputs get bf16_rne's canonical 0x7fc0 afterwards, on the integer
+// result (a select on the float inputs could be folded away: fptrunc does not
+// define NaN payloads).  About 2.5 instructions a value instead of 6.
+__device__ inline uint32_t bf16x2_rne(float a, float b) {
+  const f32x2 v = {a, b};
+  uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  h = a != a ? (h & 0xffff0000u) | 0x7fc0u : h;
+  h = b != b ? (h & 0x0000ffffu) | 0x7fc00000u : h;
+  return h;
+}
 
 // Row padding of the quantized-activation workspace.
 constexpr int kDecodeMaxRows = 16;   // one MFMA column tile of tokens (the fused quantizer, per-channel decode)

@@ -212,9 +212,7 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __r
   for (int j = 0; j < 4; ++j) {
     const float g0 = bits_f32(gw[j] << 16), g1 = bits_f32(gw[j] & 0xffff0000u);
     const float u0 = bits_f32(uw[j] << 16), u1 = bits_f32(uw[j] & 0xffff0000u);
-    const uint32_t p0 = bf16_rne(mul_rn(silu_ref(g0), u0));
-    const uint32_t p1 = bf16_rne(mul_rn(silu_ref(g1), u1));
-    out[j] = p0 | (p1 << 16);
+    out[j] = bf16x2_rne(mul_rn(silu_ref(g0), u0), mul_rn(silu_ref(g1), u1));
   }
   float s;
   const uint2 codes = quant_group8(make_uint4(out[0], out[1], out[2], out[3]), true, HALF, &s);
@@ -250,14 +248,16 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
       zv[6] = add_rn(zv[6], b1.z); zv[7] = add_rn(zv[7], b1.w);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float p = mul_rn(wk, bf16_value(bf16_rne(zv[j])));
-      acc[j] = k ? add_rn(acc[j], p) : p;
+    for (int j = 0; j < 8; j += 2) {
+      const uint32_t zb = bf16x2_rne(zv[j], zv[j + 1]);  // z rounded to bf16, two columns at a time
+      const float p0 = mul_rn(wk, bits_f32(zb << 16)), p1 = mul_rn(wk, bits_f32(zb & 0xffff0000u));
+      acc[j] = k ? add_rn(acc[j], p0) : p0;
+      acc[j + 1] = k ? add_rn(acc[j + 1], p1) : p1;
     }
   }
   uint32_t o[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o[j] = bf16_rne(acc[2 * j]) | (static_cast<uint32_t>(bf16_rne(acc[2 * j + 1])) << 16);
+  for (int j = 0; j < 4; ++j) o[j] = bf16x2_rne(acc[2 * j], acc[2 * j + 1]);
   *reinterpret_cast<uint4*>(y + static_cast<int64_t>(t) * ldy + c) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 

@@ -66,14 +66,13 @@ __device__ inline void store8(uint16_t* row, int c, int width, uint4 v) {
 }
 
 __device__ inline uint32_t add_pair(uint32_t a, uint32_t b) {
-  return static_cast<uint32_t>(bf16_rne(add_rn(lo_bf16(a), lo_bf16(b)))) |
-         (static_cast<uint32_t>(bf16_rne(add_rn(hi_bf16(a), hi_bf16(b)))) << 16);
+  return bf16x2_rne(add_rn(lo_bf16(a), lo_bf16(b)), add_rn(hi_bf16(a), hi_bf16(b)));
 }
 
 __device__ inline uint32_t norm_pair(uint32_t v, uint32_t g, float inv, float off) {
   const float n0 = mul_rn(mul_rn(lo_bf16(v), inv), add_rn(lo_bf16(g), off));
   const float n1 = mul_rn(mul_rn(hi_bf16(v), inv), add_rn(hi_bf16(g), off));
-  return static_cast<uint32_t>(bf16_rne(n0)) | (static_cast<uint32_t>(bf16_rne(n1)) << 16);
+  return bf16x2_rne(n0, n1);
 }
 
 template <bool ADD, bool QUANT, bool HALF, bool PACKED, bool VEC>

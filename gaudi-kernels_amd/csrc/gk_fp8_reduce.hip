@@ -68,8 +68,7 @@ __global__ __launch_bounds__(256) void rank_sum_kernel(const void* __restrict__ 
       uint16_t* out = static_cast<uint16_t*>(dst) + i;
       if (VEC) {
         *reinterpret_cast<uint2*>(out) =
-            make_uint2(bf16_rne(acc[0]) | (static_cast<uint32_t>(bf16_rne(acc[1])) << 16),
-                       bf16_rne(acc[2]) | (static_cast<uint32_t>(bf16_rne(acc[3])) << 16));
+            make_uint2(bf16x2_rne(acc[0], acc[1]), bf16x2_rne(acc[2], acc[3]));
       } else {
         for (int e = 0; e < n; ++e) out[e] = bf16_rne(acc[e]);
       }

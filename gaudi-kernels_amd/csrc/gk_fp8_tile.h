@@ -76,16 +76,15 @@ __device__ inline void store_tile(uint16_t* __restrict__ y, int64_t ldy, const f
     for (int r = 0; r < 4; ++r) b[r] = (n + r < N) ? bias[n + r] : 0.0f;
   }
   uint16_t* row = y + static_cast<int64_t>(m) * ldy + n;
-  const uint16_t h0 = bf16_rne(acc[0] + b[0]), h1 = bf16_rne(acc[1] + b[1]);
-  const uint16_t h2 = bf16_rne(acc[2] + b[2]), h3 = bf16_rne(acc[3] + b[3]);
+  const uint32_t h01 = bf16x2_rne(acc[0] + b[0], acc[1] + b[1]);
+  const uint32_t h23 = bf16x2_rne(acc[2] + b[2], acc[3] + b[3]);
   if (n + 3 < N && ((reinterpret_cast<uintptr_t>(row) & 7) == 0)) {
-    *reinterpret_cast<uint2*>(row) = make_uint2(h0 | (static_cast<uint32_t>(h1) << 16),
-                                                h2 | (static_cast<uint32_t>(h3) << 16));
+    *reinterpret_cast<uint2*>(row) = make_uint2(h01, h23);
   } else {
-    if (n < N) row[0] = h0;
-    if (n + 1 < N) row[1] = h1;
-    if (n + 2 < N) row[2] = h2;
-    if (n + 3 < N) row[3] = h3;
+    if (n < N) row[0] = static_cast<uint16_t>(h01);
+    if (n + 1 < N) row[1] = static_cast<uint16_t>(h01 >> 16);
+    if (n + 2 < N) row[2] = static_cast<uint16_t>(h23);
+    if (n + 3 < N) row[3] = static_cast<uint16_t>(h23 >> 16);
   }
 }
 

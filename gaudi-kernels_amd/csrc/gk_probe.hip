@@ -5,11 +5,16 @@
 // decode kernel reads weights), four pieces in flight per lane per loop
 // step, and folds them into one word that is stored only if it takes a value
 // the data never produces (so the loads cannot be removed).
+//
+// Also a check of a hardware conversion the library relies on: the kernels'
+// bf16x2_rne (gk_fp8_internal.h: v_cvt_pk_bf16_f32 with a NaN fix-up) against
+// the software bf16_rne, over every float bit pattern.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../include/gk_probe.h"
+#include "gk_fp8_internal.h"
 
 namespace {
 
@@ -32,7 +37,29 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
   if (v == 0x9E3779B9u) sink[0] = v;
 }
 
+// Input i goes through bf16x2_rne as the low value beside input i ^ 2^31 as
+// the high one, so every bit pattern takes both positions.
+__global__ __launch_bounds__(256) void bf16x2_check_kernel(unsigned long long* __restrict__ counts) {
+  const uint64_t n = 1ull << 32, step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  unsigned long long bad = 0, seen = 0;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const uint32_t a = static_cast<uint32_t>(i), b = a ^ 0x80000000u;
+    const uint32_t h = gk::bf16x2_rne(gk::bits_f32(a), gk::bits_f32(b));
+    bad += (h & 0xffffu) != gk::bf16_rne(gk::bits_f32(a));
+    bad += (h >> 16) != gk::bf16_rne(gk::bits_f32(b));
+    seen += 2;
+  }
+  atomicAdd(&counts[0], bad);
+  atomicAdd(&counts[1], seen);
+}
+
 }  // namespace
+
+extern "C" int gk_probe_bf16x2_check(void* counts, void* stream) {
+  if (!counts || (reinterpret_cast<uintptr_t>(counts) & 7)) return 1;
+  bf16x2_check_kernel<<<4096, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<unsigned long long*>(counts));
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 extern "C" int gk_probe_stream_read(const void* src, size_t bytes, void* sink, int workgroups, void* stream) {
   if (!src || !sink || bytes < 16 || (bytes & 15) || (reinterpret_cast<uintptr_t>(src) & 15) || workgroups < 1)

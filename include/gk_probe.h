@@ -6,7 +6,14 @@
  * aligned, a multiple of 16) with `workgroups` workgroups of 256 lanes and
  * 16-byte non-temporal loads, and writes nothing to `sink` (a device word)
  * unless the data folds to a sentinel.  Asynchronous on `stream` (hipStream_t
- * as void*).  Returns 0, 1 for bad arguments, 2 for a launch error. */
+ * as void*).  Returns 0, 1 for bad arguments, 2 for a launch error.
+ *
+ * gk_probe_bf16x2_check runs the kernels' paired fp32 -> bf16 rounding (the
+ * hardware conversion plus its NaN fix-up) over all 2^32 float bit patterns,
+ * each as the low and the high value, against the software round-to-nearest-
+ * even (NaN -> 0x7fc0), and adds to `counts` (two zeroed device uint64 words,
+ * 8-byte aligned) the mismatches and the values checked (2^33).  Asynchronous;
+ * returns 0, 1 for a bad pointer, 2 for a launch error. */
 #ifndef GK_PROBE_H
 #define GK_PROBE_H
 
@@ -17,6 +24,7 @@ extern "C" {
 #endif
 
 int gk_probe_stream_read(const void* src, size_t bytes, void* sink, int workgroups, void* stream);
+int gk_probe_bf16x2_check(void* counts, void* stream);
 
 #ifdef __cplusplus
 }
