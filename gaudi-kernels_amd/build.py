@@ -83,7 +83,7 @@ PROBE_LIB = OUT_DIR / "libgk_probe.so"
 
 def build_probe(verbose=True):
     """libgk_probe.so: the streaming-read probe bench.py measures the HBM ceiling with, and the exhaustive check
-    of the kernels' hardware bf16 rounding (not the GEMM library)."""
+    of the kernels' hardware bf16 rounding and E4M3 encode (not the GEMM library)."""
     OBJ_DIR.mkdir(exist_ok=True)
     tmp = PROBE_LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), *HIPCC_FLAGS, "-shared", "-Wl,-z,defs", str(PROBE_SRC), "-o", str(tmp)]
@@ -92,7 +92,7 @@ def build_probe(verbose=True):
         raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{res.stderr}")
     os.replace(tmp, PROBE_LIB)
     have = exported_symbols(PROBE_LIB)
-    if have != ["gk_probe_bf16x2_check", "gk_probe_stream_read"]:
+    if have != ["gk_probe_bf16x2_check", "gk_probe_e4m3_check", "gk_probe_stream_read"]:
         raise RuntimeError(f"probe exports {have}")
     if verbose:
         print(f"built {PROBE_LIB}")

@@ -6,9 +6,12 @@
 // step, and folds them into one word that is stored only if it takes a value
 // the data never produces (so the loads cannot be removed).
 //
-// Also a check of a hardware conversion the library relies on: the kernels'
-// bf16x2_rne (gk_fp8_internal.h: v_cvt_pk_bf16_f32 with a NaN fix-up) against
-// the software bf16_rne, over every float bit pattern.
+// Also checks of the two hardware conversions the library relies on, against
+// the software roundings of gk_fp8_math.h: the kernels' bf16x2_rne
+// (gk_fp8_internal.h: v_cvt_pk_bf16_f32 with a NaN fix-up) against bf16_rne
+// over every float bit pattern, and the E4M3 encode of quant_group8
+// (v_cvt_pk_fp8_f32, both halves of the packed word) against e4m3_rne over
+// every fp32 with |v| <= 464.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -53,7 +56,34 @@ __global__ __launch_bounds__(256) void bf16x2_check_kernel(unsigned long long* _
   atomicAdd(&counts[1], seen);
 }
 
+// Bit patterns 0 .. 0x43E80000 (464.0) with either sign: value i in the low
+// half of the word (word_sel false) beside its negation, and again in the
+// high half (word_sel true), as quant_group8 packs its eight codes.
+__global__ __launch_bounds__(256) void e4m3_check_kernel(unsigned long long* __restrict__ counts) {
+  const uint64_t n = 0x43E80001ull, step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  unsigned long long bad = 0, seen = 0;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const float p = gk::bits_f32(static_cast<uint32_t>(i)), m = -p;
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(p, m, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(m, p, w, true);
+    const uint32_t cp = gk::e4m3_rne(p), cm = gk::e4m3_rne(m), u = static_cast<uint32_t>(w);
+    bad += (u & 0xffu) != cp;
+    bad += ((u >> 8) & 0xffu) != cm;
+    bad += ((u >> 16) & 0xffu) != cm;
+    bad += (u >> 24) != cp;
+    seen += 2;
+  }
+  atomicAdd(&counts[0], bad);
+  atomicAdd(&counts[1], seen);
+}
+
 }  // namespace
+
+extern "C" int gk_probe_e4m3_check(void* counts, void* stream) {
+  if (!counts || (reinterpret_cast<uintptr_t>(counts) & 7)) return 1;
+  e4m3_check_kernel<<<4096, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<unsigned long long*>(counts));
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 extern "C" int gk_probe_bf16x2_check(void* counts, void* stream) {
   if (!counts || (reinterpret_cast<uintptr_t>(counts) & 7)) return 1;

@@ -13,7 +13,13 @@
  * each as the low and the high value, against the software round-to-nearest-
  * even (NaN -> 0x7fc0), and adds to `counts` (two zeroed device uint64 words,
  * 8-byte aligned) the mismatches and the values checked (2^33).  Asynchronous;
- * returns 0, 1 for a bad pointer, 2 for a launch error. */
+ * returns 0, 1 for a bad pointer, 2 for a launch error.
+ *
+ * gk_probe_e4m3_check does the same for the activation quantizer's hardware
+ * E4M3 encode (both halves of the packed word) against the software
+ * round-to-nearest-even encoder on every fp32 with |v| <= 464 (the
+ * quantizer's quotients stay below it): it adds the mismatches and the
+ * values checked (2 x 0x43E80001). */
 #ifndef GK_PROBE_H
 #define GK_PROBE_H
 
@@ -25,6 +31,7 @@ extern "C" {
 
 int gk_probe_stream_read(const void* src, size_t bytes, void* sink, int workgroups, void* stream);
 int gk_probe_bf16x2_check(void* counts, void* stream);
+int gk_probe_e4m3_check(void* counts, void* stream);
 
 #ifdef __cplusplus
 }

@@ -242,7 +242,7 @@ def test_partial_finish_rejections_before_device_use():
 
 
 def test_probe_library_exports_match_its_header():
-    """libgk_probe.so (bench.py's streaming-read ceiling, the bf16 rounding check) exports exactly what
+    """libgk_probe.so (bench.py's streaming-read ceiling, the hardware conversion checks) exports exactly what
     include/gk_probe.h declares."""
     probe = os.path.join(os.path.dirname(nat.lib_path()), "libgk_probe.so")
     if not os.path.exists(probe):
@@ -251,7 +251,7 @@ def test_probe_library_exports_match_its_header():
     want = sorted(set(re.findall(r"^\s*int\s+(gk_\w+)\s*\(", text, re.MULTILINE)))
     out = subprocess.run(["nm", "-D", "--defined-only", probe], check=True, capture_output=True, text=True).stdout
     have = sorted({l.split()[-1] for l in out.splitlines() if " T " in l and l.split()[-1].startswith("gk_")})
-    assert have == want == ["gk_probe_bf16x2_check", "gk_probe_stream_read"]
+    assert have == want == ["gk_probe_bf16x2_check", "gk_probe_e4m3_check", "gk_probe_stream_read"]
     lib = ctypes.CDLL(probe)
     lib.gk_probe_stream_read.restype = ctypes.c_int
     lib.gk_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
@@ -261,3 +261,6 @@ def test_probe_library_exports_match_its_header():
     lib.gk_probe_bf16x2_check.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     assert lib.gk_probe_bf16x2_check(None, None) == 1
     assert lib.gk_probe_bf16x2_check(ctypes.c_void_p((1 << 20) + 4), None) == 1
+    lib.gk_probe_e4m3_check.restype = ctypes.c_int
+    lib.gk_probe_e4m3_check.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    assert lib.gk_probe_e4m3_check(None, None) == 1
