@@ -72,7 +72,8 @@ __device__ inline uint32_t row_max16_bits(float v) {  // v >= +0
 // over the 16 lanes (one DPP row, row_max16_bits); the fp32 quotient is act_quotient
 // (exact E4M3 codes of the IEEE quotient); the encode is the gfx950
 // v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN), which equals
-// e4m3_rne for every |v| <= 464 -- and |x / s| < 464 always holds because
+// e4m3_rne for every |v| <= 464 (checked on all of them by
+// gk_probe_e4m3_check) -- and |x / s| < 464 always holds because
 // s >= amax/448 up to two fp32 roundings.
 __device__ inline uint2 quant_group8(uint4 raw, bool live, bool half, float* scale_out) {
   float v[8];
