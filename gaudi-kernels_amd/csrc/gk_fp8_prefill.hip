@@ -107,7 +107,7 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
                                                 const int32_t* __restrict__ group_cnt, int n_groups,
                                                 int64_t w_stride, int64_t sw_stride, int kparts,
                                                 float* __restrict__ yp, int64_t ldq, int gs, int64_t ldyp,
-                                                int accum) {
+                                                int accum, int xcd_cus) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
@@ -116,11 +116,33 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   static_assert(!(GROUPED && WPACK) || NA == 4, "panel-major experts come in 256-row panels");
   const int tiles_m = Mpad / kBM;
   const int tiles = tiles_m * ((N + BN - 1) / BN);
-  const int part = block / tiles, bid = block % tiles;
+  const int tiles_nn = (N + BN - 1) / BN;
+  int part = block / tiles, bid = block % tiles;
+  if (GROUPED && xcd_cus <= 0 && block >= tiles * kparts) return;  // the grid's round-up to a multiple of 8
+  if (GROUPED && xcd_cus > 0) {
+    // A grouped grid whose live (tile, K part) pairs fit one round of the
+    // xcd_cus CUs: pair l of the expert-major order (tile, then part, then
+    // column panel) goes to workgroup 8 (l % q) + l / q, q = ceil(live / 8).
+    // The hardware places workgroup b on XCD b % 8, so each XCD holds q
+    // consecutive pairs -- one expert segment's workgroups share an L2 and
+    // fetch its activation rows once, not once per XCD.  A bijection on the
+    // live pairs wherever the workgroups run; the grid is a multiple of 8 and
+    // its other workgroups exit.
+    const int per = tiles_nn * kparts;
+    const int pairs = (group_off[n_groups] / kBM) * per;
+    if (pairs <= xcd_cus) {
+      const int q = (pairs + 7) >> 3, l = (block & 7) * q + (block >> 3);
+      if ((block >> 3) >= q || l >= pairs) return;
+      const int t = l / per, r = l - t * per;
+      part = r / tiles_nn;
+      bid = t * tiles_nn + (r - part * tiles_nn);
+    } else if (block >= tiles * kparts) {
+      return;
+    }
+  }
   // Dense: consecutive workgroups share the weight panel.  Grouped: they take
   // consecutive panels of one expert segment, whose activation tiles then stay
   // in L2 (measured on MI355X, config 5 MoE layer: 482 -> 456 us).
-  const int tiles_nn = (N + BN - 1) / BN;
   const int tn = GROUPED ? bid % tiles_nn : bid / tiles_m, tm = GROUPED ? bid / tiles_nn : bid % tiles_m;
   const int n0 = tn * BN, m0 = tm * kBM;
   int live = M - m0;                       // rows of this tile whose outputs are used
@@ -491,10 +513,10 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
                                                               const int32_t* __restrict__ group_cnt, int n_groups,
                                                               int64_t w_stride, int64_t sw_stride, int kparts,
                                                               float* __restrict__ yp, int64_t ldq, int gs,
-                                                              int64_t ldyp, int accum) {
+                                                              int64_t ldyp, int accum, int xcd_cus) {
   prefill256_body<HALF, GROUPED, CH, WPACK, NA>(static_cast<int>(blockIdx.x), qa, sa, w, sw, bias, y, ldy, M, N, K,
                                                 G, Mpad, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts,
-                                                yp, ldq, gs, ldyp, accum);
+                                                yp, ldq, gs, ldyp, accum, xcd_cus);
 }
 
 // A dense GEMM in two column ranges, one launch: workgroups [0, split) take
@@ -513,10 +535,10 @@ __global__ __launch_bounds__(512) void gemm_prefill256_split_kernel(
   const int b = static_cast<int>(blockIdx.x);
   if (b < split)
     prefill256_body<HALF, false, false, WPACK, 4>(b, qa, sa, w1, sw1, bias1, y1, ldy, M, n1, K, G, Mpad, nullptr,
-                                                  nullptr, 0, 0, 0, 1, yp1, 0, gs, ldyp, accum);
+                                                  nullptr, 0, 0, 0, 1, yp1, 0, gs, ldyp, accum, 0);
   else
     prefill256_body<HALF, false, false, WPACK, 3>(b - split, qa, sa, w2, sw2, bias2, y2, ldy, M, n2, K, G, Mpad,
-                                                  nullptr, nullptr, 0, 0, 0, 1, yp2, 0, gs, ldyp, accum);
+                                                  nullptr, nullptr, 0, 0, 0, 1, yp2, 0, gs, ldyp, accum, 0);
 }
 
 // The 160 KB of dynamic LDS is above the default limit: raise it once per device.
@@ -570,28 +592,6 @@ hipError_t launch_split(const GemmArgs& a, int wide, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <bool HALF, bool GROUPED, bool WPACK = false, int NA = 4>
-hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
-                     int64_t w_stride, int64_t sw_stride, int kparts, float* yp, int64_t ldyp, hipStream_t stream) {
-  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK, NA>();
-  if (e != hipSuccess) return e;
-  constexpr int BN = 64 * NA;
-  const unsigned tiles = static_cast<unsigned>(((a.N + BN - 1) / BN) * (a.Mpad / kBM));
-  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK, NA><<<tiles * kparts, 512, kLdsBytes, stream>>>(
-      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
-      w_stride, sw_stride, kparts, yp, 0, a.gstride(), ldyp, a.accumulate ? 1 : 0);
-  return hipGetLastError();
-}
-
-template <int NA>
-hipError_t launch_dense(const GemmArgs& a, hipStream_t stream) {
-  if (a.wpack)
-    return a.half_w ? launch256<true, false, true, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
-                    : launch256<false, false, true, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
-  return a.half_w ? launch256<true, false, false, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
-                  : launch256<false, false, false, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
-}
-
 // Compute units of the current device (cached per device; 0 if unknown).
 std::once_flag g_cu_once[kMaxDevices];
 int g_cus[kMaxDevices];
@@ -605,6 +605,32 @@ int device_cus() {
   });
   return g_cus[dev];
 }
+
+template <bool HALF, bool GROUPED, bool WPACK = false, int NA = 4>
+hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
+                     int64_t w_stride, int64_t sw_stride, int kparts, float* yp, int64_t ldyp, hipStream_t stream) {
+  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK, NA>();
+  if (e != hipSuccess) return e;
+  constexpr int BN = 64 * NA;
+  const unsigned tiles = static_cast<unsigned>(((a.N + BN - 1) / BN) * (a.Mpad / kBM));
+  // grouped: the XCD placement of one-round grids (a grid of a multiple of 8)
+  const int xcd_cus = GROUPED ? device_cus() : 0;
+  const unsigned grid = GROUPED ? (tiles * kparts + 7) / 8 * 8 : tiles * kparts;
+  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK, NA><<<grid, 512, kLdsBytes, stream>>>(
+      a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
+      w_stride, sw_stride, kparts, yp, 0, a.gstride(), ldyp, a.accumulate ? 1 : 0, xcd_cus);
+  return hipGetLastError();
+}
+
+template <int NA>
+hipError_t launch_dense(const GemmArgs& a, hipStream_t stream) {
+  if (a.wpack)
+    return a.half_w ? launch256<true, false, true, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
+                    : launch256<false, false, true, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
+  return a.half_w ? launch256<true, false, false, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream)
+                  : launch256<false, false, false, NA>(a, nullptr, nullptr, 0, 0, 0, 1, a.yp, a.ldyp, stream);
+}
+
 
 }  // namespace
 
@@ -643,7 +669,7 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
   const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (mpad / kBM));
   gemm_prefill256_kernel<false, false, true><<<tiles, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, mpad, nullptr, nullptr, 0, 0, 0, 1, nullptr,
-      a.ldq, a.G, 0, 0);
+      a.ldq, a.G, 0, 0, 0);
   return hipGetLastError();
 }
 
