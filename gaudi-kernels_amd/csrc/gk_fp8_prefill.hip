@@ -29,7 +29,9 @@
 //     MFMAs.  The fragment of block j + 1 is read while block j's MFMAs run
 //     (a partial lgkmcnt wait), and block j - 1 is promoted after block j's
 //     MFMAs are issued, so the promotion FMAs never wait on the MFMA they
-//     follow.  When all of a wave's token blocks are live the step is
+//     follow; block 7's promotion waits for the next step's block 0 (past the
+//     barrier and the first fragment reads; each output element still adds its
+//     groups in order).  When all of a wave's token blocks are live the step is
 //     straight-line code, which the scheduler interleaves freely.
 //   * 16x16 output layout: lane l, register r -> n = 4 (l/16) + r, m = l % 16:
 //     one token per lane, so the promotion factor is one scalar per block.
@@ -336,6 +338,10 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
     issue_w(min(gbeg + 1, gend - 1), 1);
     int ws = 0, as = 0;  // stages of step g
     int g = gbeg;
+    v4f t[2][NA];
+    float pf7[NA];  // the promotion factors of the previous step's block 7 (deferred past the barrier)
+#pragma unroll
+    for (int i = 0; i < NA; ++i) pf7[i] = 0.0f;
     do {
       // native_half doubles the weight scales (block_fp8_oracle.py:35); x2 is exact.
       float swg[NA];  // weight scales of step g (promotion factor of block (i, j): svg[j] * swg[i])
@@ -393,7 +399,6 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
         constexpr int u = decltype(uc)::value;
         b[u] = lds_frag_at<u * kJB>(B0, B1);
       }, std::make_integer_sequence<int, kNB - 1>{});
-      v4f t[2][NA];
       unroll_each([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         // Expert segments (GROUPED) often end inside a wave's rows: there the
@@ -436,14 +441,21 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
           if (j > 0) {
 #pragma unroll
             for (int i = 0; i < NA; ++i) promote4(acc[i][j - 1], t[(j - 1) & 1][i], svg[j - 1] * swg[i]);
+          } else if (g > gbeg) {
+#pragma unroll
+            for (int i = 0; i < NA; ++i) promote4(acc[i][7], t[1][i], pf7[i]);
           }
         }
       }, std::make_integer_sequence<int, 8>{});
       if (!CH && !GROUPED) {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) promote4(acc[i][7], t[1][i], svg[7] * swg[i]);
+        for (int i = 0; i < NA; ++i) pf7[i] = svg[7] * swg[i];
       }
     } while (++g < gend);
+    if (!CH && !GROUPED) {
+#pragma unroll
+      for (int i = 0; i < NA; ++i) promote4(acc[i][7], t[1][i], pf7[i]);
+    }
   }
 
   __builtin_amdgcn_s_waitcnt(0);  // the re-read weight loads still in flight write LDS
