@@ -863,7 +863,7 @@ namespace {
 struct MoeLayout {
   int64_t rows;  // padded rows (multiple of 256)
   int kparts;    // K split of the down GEMM (fp32 partial planes of z)
-  size_t ids, wts, row_of, row_token, off, cnt, q1, sa1, hpre, q2, sa2, z, total;  // byte offsets
+  size_t ids, wts, row_of, row_token, off, cnt, q1, sa1, q2, sa2, z, total;  // byte offsets
 };
 
 gk_status moe_rows(int64_t T, int64_t E, int top_k, int64_t* rows) {
@@ -875,7 +875,7 @@ gk_status moe_rows(int64_t T, int64_t E, int top_k, int64_t* rows) {
 
 gk_status moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, MoeLayout* L) {
   if (H < 128 || I < 128 || H % 128 || I % 128 || H > kMaxDim || I > kMaxDim / 2) return GK_INCOMPATIBLE_INPUT_SIZE;
-  // the gather and SiLU quantizers take one grid row (gridDim.y <= 65535) per 128-column group
+  // the gather quantizer takes one grid row (gridDim.y <= 65535) per 128-column group
   if (H / 128 > 65535 || I / 128 > 65535) return GK_INCOMPATIBLE_INPUT_SIZE;
   gk_status st = moe_rows(T, E, top_k, &L->rows);
   if (st != GK_SUCCESS) return st;
@@ -892,7 +892,6 @@ gk_status moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, MoeL
   L->cnt = take(static_cast<size_t>(E) * 4);
   L->q1 = take(R * static_cast<size_t>(H));
   L->sa1 = take(R * static_cast<size_t>(H / 128) * 4);
-  L->hpre = take(R * static_cast<size_t>(2 * I) * 2);
   L->q2 = take(R * static_cast<size_t>(I));
   L->sa2 = take(R * static_cast<size_t>(I / 128) * 4);
   // The down GEMM has (rows / 256) * ceil(H / 256) workgroups at most: below two
@@ -977,17 +976,16 @@ gk_status gk_fp8_moe_bf16(const void* x, int64_t T, int64_t H, int64_t ldx, cons
   e = gk::launch_act_quant_rows(static_cast<const uint16_t*>(x), ldx, static_cast<int>(H), r.row_of,
                                 static_cast<int>(T), top_k, R, q1, sa1, half, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
-  uint16_t* hpre = reinterpret_cast<uint16_t*>(ws + L.hpre);
-  gk::GemmArgs a{};
-  a.qa = q1; a.sa = sa1; a.w = static_cast<const uint8_t*>(w_gu); a.sw = s_gu; a.bias = nullptr;
-  a.y = hpre; a.ldy = 2 * I; a.M = R; a.N = static_cast<int>(2 * I); a.K = static_cast<int>(H);
-  a.G = static_cast<int>(H / 128); a.Mpad = R; a.half_w = half; a.wpack = wpack;
-  e = gk::launch_gemm_grouped256(a, r.off, r.cnt, static_cast<int>(E), 1, nullptr, s);
-  if (e != hipSuccess) return GK_DEVICE_ERROR;
+  // gate_up GEMM with the SiLU-and-mul and the 1x128 quantizer in its
+  // epilogue: the down GEMM's codes and scales, no bf16 intermediate
   uint8_t* q2 = ws + L.q2;
   float* sa2 = reinterpret_cast<float*>(ws + L.sa2);
-  e = gk::launch_silu_mul_quant(hpre, 2 * I, static_cast<int>(I), r.row_of, static_cast<int>(T) * top_k, R, q2, sa2,
-                                half, s);
+  gk::GemmArgs a{};
+  a.qa = q1; a.sa = sa1; a.w = static_cast<const uint8_t*>(w_gu); a.sw = s_gu; a.bias = nullptr;
+  a.y = nullptr; a.ldy = 0; a.M = R; a.N = static_cast<int>(2 * I); a.K = static_cast<int>(H);
+  a.G = static_cast<int>(H / 128); a.Mpad = R; a.half_w = half; a.wpack = wpack;
+  a.swiglu_q = q2; a.swiglu_s = sa2;
+  e = gk::launch_gemm_grouped256(a, r.off, r.cnt, static_cast<int>(E), 1, nullptr, s);
   if (e != hipSuccess) return GK_DEVICE_ERROR;
   float* z = reinterpret_cast<float*>(ws + L.z);
   gk::GemmArgs d{};

@@ -19,21 +19,7 @@ namespace gk {
 
 namespace {
 
-// Gated activations: out = bf16(act(gate) * up), the product in fp32.
-enum Act { kSilu = 0, kGeluErf = 1, kGeluTanh = 2 };
-
-template <int ACT>
-__device__ inline float act_ref(float g) {
-  return ACT == kSilu ? silu_ref(g) : ACT == kGeluErf ? gelu_erf_ref(g) : gelu_tanh_ref(g);
-}
-
-template <int ACT>
-__device__ inline uint32_t act_mul_pair(uint32_t g2, uint32_t u2) {
-  const float g0 = bits_f32(g2 << 16), g1 = bits_f32(g2 & 0xffff0000u);
-  const float u0 = bits_f32(u2 << 16), u1 = bits_f32(u2 & 0xffff0000u);
-  return bf16x2_rne(mul_rn(act_ref<ACT>(g0), u0), mul_rn(act_ref<ACT>(g1), u1));
-}
-
+// Gated activations: out = bf16(act(gate) * up), the product in fp32 (act_mul_pair).
 template <int ACT>
 __device__ inline uint16_t act_mul_one(uint16_t g, uint16_t u) {
   return bf16_rne(mul_rn(act_ref<ACT>(bf16_value(g)), bf16_value(u)));

@@ -30,6 +30,26 @@ __device__ inline uint32_t bf16x2_rne(float a, float b) {
   return h;
 }
 
+// Gated activations: bf16(act(gate) * up) on two packed bf16 pairs, the
+// product in fp32 -- the reference's fused SiLU-and-mul
+// (csrc/tpc/generic_dense/silu_and_mul_bf16.c:4-15), whose only rounding is
+// the final product, and its GELU forms.  Shared by the separate gated
+// activation kernels and the grouped GEMM's fused SiLU-and-mul epilogue, so
+// both give the same bits.
+enum Act { kSilu = 0, kGeluErf = 1, kGeluTanh = 2 };
+
+template <int ACT>
+__device__ inline float act_ref(float g) {
+  return ACT == kSilu ? silu_ref(g) : ACT == kGeluErf ? gelu_erf_ref(g) : gelu_tanh_ref(g);
+}
+
+template <int ACT>
+__device__ inline uint32_t act_mul_pair(uint32_t g2, uint32_t u2) {
+  const float g0 = bits_f32(g2 << 16), g1 = bits_f32(g2 & 0xffff0000u);
+  const float u0 = bits_f32(u2 << 16), u1 = bits_f32(u2 & 0xffff0000u);
+  return bf16x2_rne(mul_rn(act_ref<ACT>(g0), u0), mul_rn(act_ref<ACT>(g1), u1));
+}
+
 // Row padding of the quantized-activation workspace.
 constexpr int kDecodeMaxRows = 16;   // one MFMA column tile of tokens (the fused quantizer, per-channel decode)
 constexpr int kDecodeMaxTokens = 64;  // decode variant: M <= 64 in 1, 2 or 4 column tiles (Mpad = 16, 32, 64)
@@ -209,6 +229,13 @@ struct GemmArgs {
   float* yp = nullptr;
   int64_t ldyp = 0;
   bool accumulate = false;
+  // Grouped 256 x 256 kernel only: SiLU-and-mul + 1x128 quantization fused into
+  // the epilogue.  The weights hold N = 2 * inter rows (gate rows, then up
+  // rows); instead of y the kernel writes the codes of bf16(silu(gate) * up)
+  // to swiglu_q [inter/128][Mpad][128] and their scales to swiglu_s
+  // [inter/128][Mpad] (the layout of launch_act_quant), live rows only.
+  uint8_t* swiglu_q = nullptr;
+  float* swiglu_s = nullptr;
 };
 
 hipError_t launch_gemm_decode(const GemmArgs& a, hipStream_t stream);
@@ -225,7 +252,8 @@ inline bool prefill256_fits(const GemmArgs& a) {
 // segment e starts at group_off[e] (multiple of 256) and holds group_cnt[e]
 // live rows; 32-row blocks past the live rows are skipped.  yp == nullptr:
 // bf16 y; otherwise fp32 planes yp[part][M][N] (a.y unused), one per K part
-// (kparts = 1 or 2; 2 splits the groups in halves).
+// (kparts = 1 or 2; 2 splits the groups in halves).  a.swiglu_q: the fused
+// SiLU-and-mul quantizer output instead (kparts = 1, no yp, N % 256 == 0).
 hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt,
                                   int n_groups, int kparts, float* yp, hipStream_t stream);
 hipError_t launch_gemm_generic(const GemmArgs& a, hipStream_t stream);
@@ -283,8 +311,6 @@ constexpr int kMoeMaxExperts = 256;
 hipError_t launch_moe_route(const float* logits, int T, int E, int64_t ld_logits, int top_k, int rows_max,
                             const MoeRouting& r, hipStream_t stream);
 hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const int32_t* row_of, int T, int top_k,
-                                 int rows, uint8_t* q, float* sa, bool half, hipStream_t stream);
-hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* row_of, int slots,
                                  int rows, uint8_t* q, float* sa, bool half, hipStream_t stream);
 // z: kparts fp32 planes [kparts][rows][H] of the down GEMM; y[t] = bf16(sum_k w_k bf16(sum_p z_p[row])).
 hipError_t launch_moe_combine(const float* z, int kparts, int64_t plane, int H, const int32_t* row_of,

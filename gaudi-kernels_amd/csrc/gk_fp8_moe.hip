@@ -1,6 +1,7 @@
 // Block-FP8 MoE layer kernels for gfx950: routing, row gather + 1x128
-// quantization, fused SiLU-and-mul + quantization, weighted combine.  The
-// expert GEMMs are the grouped 256 x 256 kernel (gk_fp8_prefill.hip).
+// quantization, weighted combine.  The expert GEMMs are the grouped 256 x 256
+// kernel (gk_fp8_prefill.hip); the gate_up GEMM's epilogue applies the
+// SiLU-and-mul and the 1x128 quantizer of the down GEMM's activations.
 //
 // The reference has no MoE code for this path; the layer follows BASELINE.json's
 // config 5 and is build-defined (the CPU restatement is oracle/moe.py):
@@ -188,39 +189,6 @@ __global__ __launch_bounds__(256) void act_quant_rows_kernel(const uint16_t* __r
   }
 }
 
-// ---- fused SiLU-and-mul + 1x128 quantization ----------------------------------------
-// h: bf16 [rows, 2*inter] (gate | up); one 16-lane set per (routed slot,
-// group): row row_of[slot] (padding rows, whose gate_up outputs are not
-// defined, are never visited).
-// Lane: 8 gate and 8 up values of one 128-column group -> 8 bf16 products -> codes.
-template <bool HALF>
-__global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t* __restrict__ h, int64_t ldh, int inter,
-                                                             const int32_t* __restrict__ row_of, int slots,
-                                                             int rows, uint8_t* __restrict__ q,
-                                                             float* __restrict__ sa) {
-  // grid: x = 16 slots per block, y = group (no division for the indices)
-  const int i = static_cast<int>(blockIdx.x) * (blockDim.x >> 4) + (threadIdx.x >> 4);
-  const int g = static_cast<int>(blockIdx.y), sub = threadIdx.x & 15;
-  if (i >= slots) return;  // a whole 16-lane group leaves together
-  const int64_t row = row_of[i];
-  const uint16_t* hr = h + row * ldh + g * 128 + sub * 8;
-  const uint4 gv = *reinterpret_cast<const uint4*>(hr);
-  const uint4 uv = *reinterpret_cast<const uint4*>(hr + inter);
-  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-  uint32_t out[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float g0 = bits_f32(gw[j] << 16), g1 = bits_f32(gw[j] & 0xffff0000u);
-    const float u0 = bits_f32(uw[j] << 16), u1 = bits_f32(uw[j] & 0xffff0000u);
-    out[j] = bf16x2_rne(mul_rn(silu_ref(g0), u0), mul_rn(silu_ref(g1), u1));
-  }
-  float s;
-  const uint2 codes = quant_group8(make_uint4(out[0], out[1], out[2], out[3]), true, HALF, &s);
-  const int64_t slot = static_cast<int64_t>(g) * rows + row;
-  *reinterpret_cast<uint2*>(q + slot * 128 + sub * 8) = codes;
-  if (sub == 0) sa[slot] = s;
-}
-
 // ---- combine: y[t] = bf16(w_0 z_0 + w_1 z_1), 8 columns per thread -------------------
 // z_k = bf16(sum_p zp[p][row_of[t, k]]): the down GEMM's output rounded to bf16
 // once, from its kparts fp32 partial planes.
@@ -277,16 +245,6 @@ hipError_t launch_act_quant_rows(const uint16_t* x, int64_t ldx, int K, const in
     act_quant_rows_kernel<true><<<grid, 256, 0, stream>>>(x, ldx, row_of, T, top_k, rows, q, sa);
   else
     act_quant_rows_kernel<false><<<grid, 256, 0, stream>>>(x, ldx, row_of, T, top_k, rows, q, sa);
-  return hipGetLastError();
-}
-
-hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int inter, const int32_t* row_of, int slots,
-                                 int rows, uint8_t* q, float* sa, bool half, hipStream_t stream) {
-  const dim3 grid((slots + 15) / 16, inter / 128);
-  if (half)
-    silu_mul_quant_kernel<true><<<grid, 256, 0, stream>>>(h, ldh, inter, row_of, slots, rows, q, sa);
-  else
-    silu_mul_quant_kernel<false><<<grid, 256, 0, stream>>>(h, ldh, inter, row_of, slots, rows, q, sa);
   return hipGetLastError();
 }
 

@@ -94,13 +94,25 @@ constexpr int kLdsBytes = (kWStages + kAStages) * kTile;  // 160 KB: all of the 
 // tile is one contiguous run (measured on MI355X, config 5 gate_up: 259 ->
 // 243 us; in the tile-major order a step reads 16 pieces 64 KB apart).
 //
+// SWI (grouped, NA = 4): SiLU-and-mul + 1x128 quantization fused into the
+// epilogue of a gate_up GEMM, whose N = 2 inter weight rows are the gate rows
+// then the up rows.  Tile tn loads gate rows [128 tn, +128) as its rows 0..127
+// and up rows [inter + 128 tn, +128) as rows 128..255, so waves wn = 0, 1 hold
+// gate columns and waves wn = 2, 3 the up columns of the same rows and
+// columns, in the same lane layout.  The epilogue rounds both to bf16 (as the
+// bf16 store does), meets them in LDS and quantizes h = bf16(silu(g) * u)
+// with the same per-lane arithmetic as the separate fused quantizer, into
+// group tn of swq [inter/128][Mpad][128] / sws [inter/128][Mpad]: h is never
+// written to memory (measured on MI355X, config 5 MoE layer: the 59 MB bf16
+// round trip and its 21 us kernel go).
+//
 // NA: 16-row weight blocks per wave; the tile is 64 NA weight rows (256, or
 // 192 for the narrow tiles that fill the last round of a large GEMM).  A
 // 48-row wave can straddle two 128-row scale blocks, so NA = 3 takes one
 // weight scale per block.
 // The workgroup body; `block` is the workgroup's index within its launch (or
 // within its column range of the split launch below).
-template <bool HALF, bool GROUPED, bool CH, bool WPACK, int NA>
+template <bool HALF, bool GROUPED, bool CH, bool WPACK, int NA, bool SWI = false>
 __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __restrict__ qa,
                                                 const float* __restrict__ sa, const uint8_t* __restrict__ w,
                                                 const float* __restrict__ sw, const float* __restrict__ bias,
@@ -109,13 +121,15 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
                                                 const int32_t* __restrict__ group_cnt, int n_groups,
                                                 int64_t w_stride, int64_t sw_stride, int kparts,
                                                 float* __restrict__ yp, int64_t ldq, int gs, int64_t ldyp,
-                                                int accum, int xcd_cus) {
+                                                int accum, int xcd_cus, uint8_t* __restrict__ swq = nullptr,
+                                                float* __restrict__ sws = nullptr) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it are scalar
   const int wn = wave & 3, wm = wave >> 2;
   constexpr int BN = 64 * NA;  // weight rows of the tile
   static_assert(!(GROUPED && WPACK) || NA == 4, "panel-major experts come in 256-row panels");
+  static_assert(!SWI || (GROUPED && !CH && NA == 4), "the fused SiLU-and-mul epilogue is a grouped 256-row form");
   const int tiles_m = Mpad / kBM;
   const int tiles = tiles_m * ((N + BN - 1) / BN);
   const int tiles_nn = (N + BN - 1) / BN;
@@ -174,7 +188,14 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   // group-major activations two (the chunk key of rows r0 + 8 i alternates with
   // i % 2); row-major weights and per-token activations clamp every row, so
   // they keep one offset per instruction.
-  const uint8_t* asrc = w + static_cast<int64_t>(n0) * K;  // packed: tile n0/16 starts at (n0/16) * G * 2048 = n0 * K
+  // SWI: weight row of this wave's first loaded tile row 32 wave (tile rows
+  // 0..127 are gate rows 128 tn + r, rows 128..255 up rows inter + 128 tn + r - 128;
+  // a wave's 32 rows lie in one 256-row panel).  Row-major weights start the
+  // wave's view at tile row 0's weight row, packed ones at its panel.
+  const int swrow = SWI ? (wave < 4 ? 128 * tn : (N >> 1) + 128 * tn - 128) + 32 * wave : 0;
+  const int64_t wrow0 = SWI ? (WPACK ? (swrow & ~255) : swrow - 32 * wave) : n0;
+  const int sblk = SWI ? (swrow & 255) >> 4 : 0;  // SWI, packed: the wave's first 16-row block in its panel
+  const uint8_t* asrc = w + wrow0 * K;  // packed: tile n0/16 starts at (n0/16) * G * 2048 = n0 * K
   const uint8_t* bsrc = qa + static_cast<int64_t>(m0) * (CH ? ldq : 128);
   const int nmax = N - 1 - n0, mmax = M - 1 - m0;
   const int nblk = ((N + 15) >> 4) - 1 - (n0 >> 4);  // last 16-row block of the panel
@@ -210,7 +231,7 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
     uint32_t vo, so;
     if (WPACK) {
       const int p = NA * wave + i;
-      const int blk = min(p >> 1, nblk);
+      const int blk = SWI ? sblk + (i >> 1) : min(p >> 1, nblk);
       vo = lane16;
       so = static_cast<uint32_t>((GROUPED ? g * nbp + blk : blk * gs + g) * 2048 + (p & 1) * 1024);
     } else {
@@ -281,7 +302,8 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   const float* swp[kScales];
 #pragma unroll
   for (int i = 0; i < kScales; ++i)
-    swp[i] = sw + static_cast<int64_t>(min(n0 + wn * 16 * NA + 16 * i, N - 1) >> 7) * gs;
+    swp[i] = sw + static_cast<int64_t>(SWI ? (wn < 2 ? tn : (N >> 8) + tn)
+                                           : min(n0 + wn * 16 * NA + 16 * i, N - 1) >> 7) * gs;
   float* ypp = yp ? yp + static_cast<int64_t>(part) * M * ldyp : nullptr;
   // the wave's blocks that hold live rows: j < jl (wave-uniform)
   const int jl = min(8, max(0, (live - mw + kJS - 1) / kJS));
@@ -438,7 +460,7 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
           }
         } else {
           block_mfma(a, b[j % kNB], t[j & 1]);
-          if (j > 0) {
+          if constexpr (j > 0) {
 #pragma unroll
             for (int i = 0; i < NA; ++i) promote4(acc[i][j - 1], t[(j - 1) & 1][i], svg[j - 1] * swg[i]);
           } else if (g > gbeg) {
@@ -459,6 +481,46 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   }
 
   __builtin_amdgcn_s_waitcnt(0);  // the re-read weight loads still in flight write LDS
+
+  if (SWI) {
+    // gate (waves wn = 0, 1) and up (wn = 2, 3) outputs, bf16-rounded as
+    // store_tile rounds them, into LDS [2][256 rows][256 B]: 16-byte chunk c
+    // of row m at slot c ^ (m & 15), so a wave's 8-byte writes (16 rows x 2
+    // halves of one chunk per 32 lanes) and the 16-lane reads of a row hit
+    // distinct banks.  Rows past the live rows are never read.
+    __syncthreads();  // every wave's fragment reads are done (the tile copies: waitcnt above)
+    const uint32_t hbase = static_cast<uint32_t>(wn >> 1) << 16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < jl) {
+        const int ml = mw + j * kJS + fr;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+          const int c = 8 * (wn & 1) + 2 * i + (fq >> 1);
+          const v4f v = acc[i][j];
+          *reinterpret_cast<uint2*>(smem + hbase + ml * 256 + ((c ^ (ml & 15)) << 4) + (fq & 1) * 8) =
+              make_uint2(bf16x2_rne(v[0] + 0.0f, v[1] + 0.0f), bf16x2_rne(v[2] + 0.0f, v[3] + 0.0f));
+        }
+      }
+    }
+    __syncthreads();
+    // 16 lanes per live row: 8 gate and 8 up values each -> 8 bf16 products
+    // -> the row's 128-column group quantized (a 16-lane set leaves together)
+    const int rows = min(live, kBM), sub = tid & 15;
+    for (int r = tid >> 4; r < rows; r += 32) {
+      const uint32_t o = static_cast<uint32_t>(r * 256 + ((sub ^ (r & 15)) << 4));
+      const uint4 gv = *reinterpret_cast<const uint4*>(smem + o);
+      const uint4 uv = *reinterpret_cast<const uint4*>(smem + 65536 + o);
+      const uint4 h = make_uint4(act_mul_pair<kSilu>(gv.x, uv.x), act_mul_pair<kSilu>(gv.y, uv.y),
+                                 act_mul_pair<kSilu>(gv.z, uv.z), act_mul_pair<kSilu>(gv.w, uv.w));
+      float s;
+      const uint2 codes = quant_group8(h, true, HALF, &s);
+      const int64_t slot = static_cast<int64_t>(tn) * Mpad + m0 + r;
+      *reinterpret_cast<uint2*>(swq + slot * 128 + sub * 8) = codes;
+      if (sub == 0) sws[slot] = s;
+    }
+    return;
+  }
 
   if (CH) {
 #pragma unroll
@@ -513,7 +575,7 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
   }
 }
 
-template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4, bool SWI = false>
 __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __restrict__ qa,
                                                               const float* __restrict__ sa,
                                                               const uint8_t* __restrict__ w,
@@ -525,10 +587,11 @@ __global__ __launch_bounds__(512) void gemm_prefill256_kernel(const uint8_t* __r
                                                               const int32_t* __restrict__ group_cnt, int n_groups,
                                                               int64_t w_stride, int64_t sw_stride, int kparts,
                                                               float* __restrict__ yp, int64_t ldq, int gs,
-                                                              int64_t ldyp, int accum, int xcd_cus) {
-  prefill256_body<HALF, GROUPED, CH, WPACK, NA>(static_cast<int>(blockIdx.x), qa, sa, w, sw, bias, y, ldy, M, N, K,
-                                                G, Mpad, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts,
-                                                yp, ldq, gs, ldyp, accum, xcd_cus);
+                                                              int64_t ldyp, int accum, int xcd_cus,
+                                                              uint8_t* __restrict__ swq, float* __restrict__ sws) {
+  prefill256_body<HALF, GROUPED, CH, WPACK, NA, SWI>(static_cast<int>(blockIdx.x), qa, sa, w, sw, bias, y, ldy, M,
+                                                     N, K, G, Mpad, group_off, group_cnt, n_groups, w_stride,
+                                                     sw_stride, kparts, yp, ldq, gs, ldyp, accum, xcd_cus, swq, sws);
 }
 
 // A dense GEMM in two column ranges, one launch: workgroups [0, split) take
@@ -556,19 +619,21 @@ __global__ __launch_bounds__(512) void gemm_prefill256_split_kernel(
 // The 160 KB of dynamic LDS is above the default limit: raise it once per device.
 constexpr int kMaxDevices = 64;
 
-std::once_flag g_lds_once[kMaxDevices][36];
-hipError_t g_lds_err[kMaxDevices][36];
+std::once_flag g_lds_once[kMaxDevices][40];
+hipError_t g_lds_err[kMaxDevices][40];
 
-template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4>
+template <bool HALF, bool GROUPED, bool CH = false, bool WPACK = false, int NA = 4, bool SWI = false>
 hipError_t ensure_lds_limit() {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  constexpr int slot = (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0) + (WPACK ? 8 : 0) + (NA == 3 ? 16 : 0);
+  // slots 32..35: the split kernel; 36..39: the fused SiLU-and-mul form (grouped, NA = 4)
+  constexpr int slot = SWI ? 36 + (HALF ? 1 : 0) + (WPACK ? 2 : 0)
+                           : (HALF ? 1 : 0) + (GROUPED ? 2 : 0) + (CH ? 4 : 0) + (WPACK ? 8 : 0) + (NA == 3 ? 16 : 0);
   std::call_once(g_lds_once[dev][slot], [dev] {
     g_lds_err[dev][slot] = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH, WPACK, NA>),
+        reinterpret_cast<const void*>(&gemm_prefill256_kernel<HALF, GROUPED, CH, WPACK, NA, SWI>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
   });
   return g_lds_err[dev][slot];
@@ -618,19 +683,19 @@ int device_cus() {
   return g_cus[dev];
 }
 
-template <bool HALF, bool GROUPED, bool WPACK = false, int NA = 4>
+template <bool HALF, bool GROUPED, bool WPACK = false, int NA = 4, bool SWI = false>
 hipError_t launch256(const GemmArgs& a, const int32_t* group_off, const int32_t* group_cnt, int n_groups,
                      int64_t w_stride, int64_t sw_stride, int kparts, float* yp, int64_t ldyp, hipStream_t stream) {
-  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK, NA>();
+  hipError_t e = ensure_lds_limit<HALF, GROUPED, false, WPACK, NA, SWI>();
   if (e != hipSuccess) return e;
   constexpr int BN = 64 * NA;
   const unsigned tiles = static_cast<unsigned>(((a.N + BN - 1) / BN) * (a.Mpad / kBM));
   // grouped: the XCD placement of one-round grids (a grid of a multiple of 8)
   const int xcd_cus = GROUPED ? device_cus() : 0;
   const unsigned grid = GROUPED ? (tiles * kparts + 7) / 8 * 8 : tiles * kparts;
-  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK, NA><<<grid, 512, kLdsBytes, stream>>>(
+  gemm_prefill256_kernel<HALF, GROUPED, false, WPACK, NA, SWI><<<grid, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, a.Mpad, group_off, group_cnt, n_groups,
-      w_stride, sw_stride, kparts, yp, 0, a.gstride(), ldyp, a.accumulate ? 1 : 0, xcd_cus);
+      w_stride, sw_stride, kparts, yp, 0, a.gstride(), ldyp, a.accumulate ? 1 : 0, xcd_cus, a.swiglu_q, a.swiglu_s);
   return hipGetLastError();
 }
 
@@ -681,7 +746,7 @@ hipError_t launch_gemm_channel256(const GemmArgs& a, hipStream_t stream) {
   const unsigned tiles = static_cast<unsigned>(((a.N + kBN - 1) / kBN) * (mpad / kBM));
   gemm_prefill256_kernel<false, false, true><<<tiles, 512, kLdsBytes, stream>>>(
       a.qa, a.sa, a.w, a.sw, a.bias, a.y, a.ldy, a.M, a.N, a.K, a.G, mpad, nullptr, nullptr, 0, 0, 0, 1, nullptr,
-      a.ldq, a.G, 0, 0, 0);
+      a.ldq, a.G, 0, 0, 0, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -709,6 +774,19 @@ hipError_t launch_gemm_grouped256(const GemmArgs& a, const int32_t* group_off, c
     return hipErrorInvalidValue;
   const int64_t w_stride = a.wpack ? packed_weight_bytes(a.N, a.K) : static_cast<int64_t>(a.N) * a.K;
   const int64_t sw_stride = static_cast<int64_t>((a.N + 127) / 128) * a.G;
+  if (a.swiglu_q) {
+    // the fused SiLU-and-mul form: gate | up halves of 128-row multiples, one K part, codes out
+    if (!a.swiglu_s || kparts != 1 || yp || a.N % 256) return hipErrorInvalidValue;
+    if (a.wpack)
+      return a.half_w ? launch256<true, true, true, 4, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride,
+                                                             1, nullptr, 0, stream)
+                      : launch256<false, true, true, 4, true>(a, group_off, group_cnt, n_groups, w_stride,
+                                                              sw_stride, 1, nullptr, 0, stream);
+    return a.half_w ? launch256<true, true, false, 4, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, 1,
+                                                            nullptr, 0, stream)
+                    : launch256<false, true, false, 4, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride,
+                                                             1, nullptr, 0, stream);
+  }
   if (a.wpack)
     return a.half_w ? launch256<true, true, true>(a, group_off, group_cnt, n_groups, w_stride, sw_stride, kparts, yp,
                                                   a.N, stream)

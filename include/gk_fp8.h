@@ -433,8 +433,9 @@ gk_status gk_fp8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ld
  * region starting at a 256-byte boundary (R = rows_max, G_H = H/128,
  * G_I = I/128): ids, wts, row_of [T*k] x 4 B; row_token [R] int32;
  * offsets [E+1] int32; counts [E] int32 (live rows of each expert); gathered
- * codes [G_H][R][128] u8 and scales [G_H][R] fp32; gate_up output bf16
- * [R][2I]; SiLU-and-mul codes [G_I][R][128] u8 and scales [G_I][R] fp32;
+ * codes [G_H][R][128] u8 and scales [G_H][R] fp32; SiLU-and-mul codes
+ * [G_I][R][128] u8 and scales [G_I][R] fp32 (the gate_up GEMM writes them
+ * from its epilogue: its bf16 output is not stored);
  * down output fp32 [P][R][H], P = 2 partial sums over the two halves of I
  * when (R/256) * ceil(H/256) < 512, else P = 1 (the layer rounds
  * sum_p z[p] to bf16 before the combine).  Only the live rows of each

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from gaudi_kernels import _native as nat
 from gaudi_kernels import ops
 from oracle import block_fp8, moe, synth
 
@@ -63,7 +64,6 @@ def test_routing_ties_and_skew():
 def test_routing_oversized_row_buffer_fully_defined():
     # row_token larger than gk_fp8_moe_rows_max: every entry past the layout reads -1
     import ctypes
-    from gaudi_kernels import _native as nat
     t, e, k = 300, 8, 2
     logits = torch.randn(t, e, generator=torch.Generator().manual_seed(11))
     rows = ops.moe_rows_max(t, e, k)
@@ -155,8 +155,7 @@ def regions(ws, t, h, inter, e, k):
     parts = 2 if (rows // 256) * ((h + 255) // 256) < 512 else 1
     sizes = [("ids", t * k * 4), ("wts", t * k * 4), ("row_of", t * k * 4), ("row_token", rows * 4),
              ("off", (e + 1) * 4), ("cnt", e * 4), ("q1", rows * h), ("sa1", rows * h // 128 * 4),
-             ("hpre", rows * 2 * inter * 2), ("q2", rows * inter), ("sa2", rows * inter // 128 * 4),
-             ("z", parts * rows * h * 4)]
+             ("q2", rows * inter), ("sa2", rows * inter // 128 * 4), ("z", parts * rows * h * 4)]
     out, at = {}, 0
     for name, nbytes in sizes:
         out[name] = ws[at:at + nbytes]
@@ -164,7 +163,8 @@ def regions(ws, t, h, inter, e, k):
     assert at == ops.moe_workspace_bytes(t, h, inter, e, k)
     v = {n: out[n].view(torch.int32) for n in ("ids", "row_of", "row_token", "off", "cnt")}
     v["wts"] = out["wts"].view(torch.float32)
-    v["hpre"] = out["hpre"].view(torch.bfloat16).reshape(rows, 2 * inter)
+    v["q1"] = out["q1"].reshape(h // 128, rows, 128)
+    v["sa1"] = out["sa1"].view(torch.float32).reshape(h // 128, rows)
     v["q2"] = out["q2"].reshape(inter // 128, rows, 128)
     v["sa2"] = out["sa2"].view(torch.float32).reshape(inter // 128, rows)
     zp = out["z"].view(torch.float32).reshape(parts, rows, h)
@@ -177,13 +177,54 @@ def regions(ws, t, h, inter, e, k):
     return {n: x.cpu() for n, x in v.items()}
 
 
+def separate_chain_check(r, rows, w_gu, s_gu, h, inter, native_half=False):
+    """The layer's SiLU-and-mul codes and scales on `rows` (one expert's routed rows) against the
+    separate chain on the layer's own gathered codes: the dense 256 x 256 GEMM (forced at any row
+    count), then the SiLU-and-mul quantizer.  Bit-identical: the dense and grouped forms of that
+    kernel give each output element the same arithmetic.  Returns the chain's gate_up output (device)."""
+    n = len(rows)
+    m_pad = ops.plan(n, 2 * inter, h, nat.GK_FLAG_FORCE_PREFILL)[1]
+    q1 = torch.zeros((h // 128, m_pad, 128), dtype=torch.uint8)
+    sa1 = torch.zeros((h // 128, m_pad), dtype=torch.float32)
+    q1[:, :n], sa1[:, :n] = r["q1"][:, rows], r["sa1"][:, rows]
+    gate_up = ops.block_fp8_gemm_q(q1.cuda(), sa1.cuda(), n, w_gu.cuda(), s_gu.cuda(), native_half=native_half,
+                                   variant="prefill")
+    q_sep, sa_sep = ops.silu_mul_quant(gate_up, native_half=native_half)
+    assert torch.equal(r["q2"][:, rows], q_sep.cpu()[:, :n])
+    assert torch.equal(r["sa2"][:, rows].view(torch.int32), sa_sep.cpu()[:, :n].view(torch.int32))
+    return gate_up
+
+
+@pytest.mark.parametrize("t,h,inter,e,k", [(300, 512, 384, 4, 2), (200, 384, 256, 3, 2), (70, 256, 128, 5, 1)])
+@pytest.mark.parametrize("native_half", [False, True])
+@pytest.mark.parametrize("packed", [False, True])
+def test_moe_fused_silu_codes_equal_separate_chain(t, h, inter, e, k, native_half, packed):
+    """The gate_up epilogue's SiLU-and-mul + 1x128 codes and scales on every routed row against the
+    separate kernels (inter 384: the up rows start half-way into a 256-row weight panel)."""
+    x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=900 + t, device="cuda")
+    ws = torch.full((ops.moe_workspace_bytes(t, h, inter, e, k),), 0xC3, dtype=torch.uint8, device="cuda")
+    w_gu = ops.pack_experts(wg) if packed else wg
+    w_dn = ops.pack_experts(wd) if packed else wd
+    ops.moe_block_fp8(x.cuda(), logits.cuda(), w_gu, sg, w_dn, sd, top_k=k, native_half=native_half, workspace=ws)
+    r = regions(ws, t, h, inter, e, k)
+    ids, row_of = r["ids"].reshape(t, k), r["row_of"].reshape(t, k)
+    for x_e in range(e):
+        rows = row_of[ids == x_e].long()
+        if len(rows):
+            separate_chain_check(r, rows, wg[x_e], sg[x_e], h, inter, native_half)
+
+
 @pytest.mark.timeout(600)
 def test_moe_config5_stagewise_parity():
     """Each stage of config 5 against the oracle, fed the device's own input to that stage, on every routed row.
 
-    gate_up and down: the GEMM gate per expert row set; SiLU-and-mul + quantization:
-    codes equal to the oracle's on the device's gate_up output except where the
-    device exp differs by an ulp; combine: bit-exact on the device's z and weights.
+    The layer's gate_up GEMM stores no bf16 output (its epilogue applies the SiLU-and-mul
+    and the quantizer), so each expert's gate_up output is recomputed by the dense GEMM on
+    the layer's own gathered codes and scales.  gate_up and down: the GEMM gate per expert
+    row set; the layer's SiLU-and-mul codes and scales: bit-identical to the separate
+    device quantizer on that output (the same per-element arithmetic in both GEMM
+    kernels), and equal to the oracle's except where the device exp differs by an ulp;
+    combine: bit-exact on the device's z and weights.
     """
     t, h, inter, e, k = 512, 4096, 14336, 8, 2
     x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=5000, device="cuda")
@@ -202,12 +243,14 @@ def test_moe_config5_stagewise_parity():
         rows = torch.tensor([int(row_of[tok, s]) for tok, s in pairs])
         toks = torch.tensor([tok for tok, _ in pairs])
         w_gu, s_gu, w_dn, s_dn = wg[x_e].cpu(), sg[x_e].cpu(), wd[x_e].cpu(), sd[x_e].cpu()
-        hpre = r["hpre"][rows]
+        n = len(rows)
+        gate_up = separate_chain_check(r, rows, wg[x_e], sg[x_e], h, inter)
+        hpre = gate_up.cpu()
         ref_gu = block_fp8.reference(x[toks], w_gu, s_gu, row_chunk=16)
         p_gu = block_fp8.parity(hpre, ref_gu)
         hq = moe.silu_mul(hpre)
         codes, sa = block_fp8.act_quant(hq)
-        got_codes = r["q2"][:, rows].permute(1, 0, 2).reshape(len(rows), -1)
+        got_codes = r["q2"][:, rows].permute(1, 0, 2).reshape(n, -1)
         mismatch = (got_codes != codes).float().mean().item()
         got_sa = r["sa2"][:, rows].T
         ref_dn = block_fp8.reference(hq, w_dn, s_dn, row_chunk=16)
@@ -228,8 +271,9 @@ def test_moe_config5_stagewise_parity():
 
 @pytest.mark.timeout(600)
 def test_moe_config5_packed_bit_identical():
-    """Config 5 with experts packed at load time against row-major experts: the gate_up output, the down
-    GEMM's fp32 K-split planes and y agree bit for bit (the grouped kernel's two weight layouts)."""
+    """Config 5 with experts packed at load time against row-major experts: the SiLU-and-mul codes and
+    scales from the gate_up epilogue, the down GEMM's fp32 K-split planes and y agree bit for bit (the
+    grouped kernel's two weight layouts)."""
     t, h, inter, e, k = 512, 4096, 14336, 8, 2
     x, logits, wg, sg, wd, sd = problem(t, h, inter, e, seed=5000, device="cuda")
     xg, lg = x.cuda(), logits.cuda()
@@ -242,7 +286,8 @@ def test_moe_config5_packed_bit_identical():
     r_row, r_pack = regions(ws_row, t, h, inter, e, k), regions(ws_pack, t, h, inter, e, k)
     rows = r_row["row_of"].long().reshape(-1)  # every routed row
     assert torch.equal(r_row["row_of"], r_pack["row_of"])
-    assert torch.equal(r_row["hpre"][rows].view(torch.int16), r_pack["hpre"][rows].view(torch.int16))
+    assert torch.equal(r_row["q2"][:, rows], r_pack["q2"][:, rows])
+    assert torch.equal(r_row["sa2"][:, rows].view(torch.int32), r_pack["sa2"][:, rows].view(torch.int32))
     assert torch.equal(r_row["zp"][:, rows].view(torch.int32), r_pack["zp"][:, rows].view(torch.int32))
     assert torch.equal(y_row.view(torch.int16), y_pack.view(torch.int16))
 
