@@ -180,6 +180,35 @@ def test_moe_route_rejections_before_device_use():
              None) == nat.GK_INCOMPATIBLE_DATA_TYPE
 
 
+@pytest.mark.parametrize("t,h,inter,e,k", [(512, 4096, 14336, 8, 2), (3, 384, 128, 8, 2), (300, 256, 128, 3, 1),
+                                           (4500, 11008, 128, 9, 2), (1, 128, 128, 256, 1)])
+def test_moe_workspace_is_the_documented_regions(t, h, inter, e, k):
+    """gk_fp8_moe_workspace_bytes = the regions include/gk_fp8.h lists for gk_fp8_moe_bf16, in order, each
+    from a 256-byte boundary (no bf16 gate_up region: its epilogue writes the SiLU-and-mul codes)."""
+    lib = nat.load()
+    rows, nbytes = ctypes.c_int64(0), ctypes.c_size_t(0)
+    assert lib.gk_fp8_moe_rows_max(t, e, k, ctypes.byref(rows)) == nat.GK_SUCCESS
+    r = rows.value
+    assert r == (t * k + 255 * e + 255) // 256 * 256
+    parts = 2 if (r // 256) * ((h + 255) // 256) < 512 else 1
+    sizes = [t * k * 4, t * k * 4, t * k * 4, r * 4, (e + 1) * 4, e * 4, r * h, r * h // 128 * 4, r * inter,
+             r * inter // 128 * 4, parts * r * h * 4]
+    assert lib.gk_fp8_moe_workspace_bytes(t, h, inter, e, k, ctypes.byref(nbytes)) == nat.GK_SUCCESS
+    assert nbytes.value == sum((n + 255) // 256 * 256 for n in sizes)
+
+
+def test_moe_workspace_rejects_bad_shapes():
+    lib = nat.load()
+    nbytes = ctypes.c_size_t(0)
+    f = lambda *a: lib.gk_fp8_moe_workspace_bytes(*a, ctypes.byref(nbytes))
+    assert f(512, 4000, 14336, 8, 2) == nat.GK_INCOMPATIBLE_INPUT_SIZE    # H not a multiple of 128
+    assert f(512, 4096, 14300, 8, 2) == nat.GK_INCOMPATIBLE_INPUT_SIZE    # I not a multiple of 128
+    assert f(512, 4096, 14336, 257, 2) == nat.GK_INCOMPATIBLE_INPUT_SIZE  # more than 256 experts
+    assert f(512, 4096, 14336, 8, 3) == nat.GK_INCOMPATIBLE_INPUT_SIZE    # top_k > 2
+    assert f(0, 4096, 14336, 8, 2) == nat.GK_INCOMPATIBLE_INPUT_SIZE      # no tokens
+    assert lib.gk_fp8_moe_workspace_bytes(512, 4096, 14336, 8, 2, None) == nat.GK_INVALID_ARGUMENT
+
+
 def test_rank_sum_rejections_before_device_use():
     """generic_dense_glue_contract_test.cpp:533-584 and the glue's checks (generic_dense_glue.cpp:568-600, 871-895)."""
     lib = nat.load()
