@@ -89,4 +89,22 @@ inline DecodeShape fused_quant_shape(DecodeShape d, int G) {
   return d;
 }
 
+// Dense 256 x 256 GEMM tile order (gk_fp8_prefill.hip).  Workgroup bid of a
+// launch (or column range) of tiles_m x tiles_nn tiles and kparts K parts runs
+// on XCD bid % 8 of the GPU.  With a multiple of 8 tiles and one K part, XCD
+// x takes the x-th eighth of the tiles in super-block order: 4 weight panels
+// (tn) by all row tiles (tm), row tile by row tile -- so the CUs of one XCD
+// share few weight panels and activation row tiles in its L2.  Returns
+// tn * 65536 + tm; a bijection on the tiles for every grid (plan_check.cpp).
+// constexpr: callable from device code.
+constexpr int dense_tile_of(int bid, int tiles_m, int tiles_nn, int kparts) {
+  const int tiles = tiles_m * tiles_nn;
+  const int l = (tiles % 8 == 0 && kparts == 1) ? (bid % 8) * (tiles / 8) + bid / 8 : bid;
+  const int sb = l / (4 * tiles_m);
+  const int left = tiles_nn - sb * 4;
+  const int wsb = left < 4 ? left : 4;
+  const int rem = l - sb * 4 * tiles_m;
+  return (sb * 4 + rem % wsb) * 65536 + rem / wsb;
+}
+
 }  // namespace gk

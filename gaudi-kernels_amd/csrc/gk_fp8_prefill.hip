@@ -156,10 +156,23 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
       return;
     }
   }
-  // Dense: consecutive workgroups share the weight panel.  Grouped: they take
-  // consecutive panels of one expert segment, whose activation tiles then stay
-  // in L2 (measured on MI355X, config 5 MoE layer: 482 -> 456 us).
-  const int tn = GROUPED ? bid % tiles_nn : bid / tiles_m, tm = GROUPED ? bid / tiles_nn : bid % tiles_m;
+  // Grouped: consecutive workgroups take consecutive panels of one expert
+  // segment, whose activation tiles then stay in L2 (measured on MI355X,
+  // config 5 MoE layer: 482 -> 456 us).  Dense: XCD-aware order.  Workgroup b
+  // runs on XCD b % 8; in a launch (or column range) of a multiple of 8 tiles,
+  // XCD x takes the x-th eighth of the tiles in super-block order (4 weight
+  // panels x all row tiles, row tile by row tile), so the CUs of one XCD share
+  // few panels and row tiles in its L2 (config 4: 4 panels x 8 row tiles per
+  // XCD instead of 16 panels x 2 row tiles): dense_tile_of (gk_fp8_plan.h).
+  int tn, tm;
+  if (GROUPED) {
+    tn = bid % tiles_nn;
+    tm = bid / tiles_nn;
+  } else {
+    const int v = dense_tile_of(bid, tiles_m, tiles_nn, kparts);
+    tn = v >> 16;
+    tm = v & 0xffff;
+  }
   const int n0 = tn * BN, m0 = tm * kBM;
   int live = M - m0;                       // rows of this tile whose outputs are used
   if (GROUPED) {
@@ -240,8 +253,14 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
     }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(wrsrc, lds_ptr(base + i * 1024), 16, vo, so, 0, 0);
   };
+  // The dense form's spread copies are issued on every path (dead rows and the
+  // last step included, clamped to rows and groups that exist), so the
+  // compiler's vmcnt waits count the same loads on every path through a step:
+  // with a conditional copy it waits for the minimum count over the paths,
+  // which at the loop's back edge meant waiting for this step's weight copies
+  // (measured on MI355X, config 4 GEMM: 197-204 -> 190-193 us with the
+  // interleaved promotion below; M = 1024, N = 4096, K = 14336: 170 -> 153 us).
   auto issue_a_one = [&](int g, int as, int i) {
-    if (!act_live) return;
     uint8_t* base = smem + (kWStages + as) * kTile + wave * 32 * 128;
     uint32_t vo, so;
     if (CH) {
@@ -429,7 +448,7 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
         const bool skip = GROUPED && j >= jl;
         if (kSpread) {  // this step's tile loads, spread over the first blocks
           if (j < 4) {
-            if (g + 1 < gend) issue_a_one(g + 1, as_next, j);
+            issue_a_one(min(g + 1, gend - 1), as_next, j);
           } else if (j - 4 < NA) {
             issue_w_one(min(g + 2, gend - 1), ws_free, j - 4);
           }
@@ -466,6 +485,15 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
           } else if (g > gbeg) {
 #pragma unroll
             for (int i = 0; i < NA; ++i) promote4(acc[i][7], t[1][i], pf7[i]);
+          }
+          // One MFMA, then the four promotion FMAs of the previous block's
+          // same weight fragment: the matrix core and the VALU work side by
+          // side (a microbenchmark of this mix on MI355X: 85% -> 90% of the
+          // FP8 peak at two waves per SIMD).
+#pragma unroll
+          for (int i = 0; i < NA; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
           }
         }
       }, std::make_integer_sequence<int, 8>{});

@@ -37,5 +37,26 @@ int main() {
             "token-channel gemm", n, g, 1, 0);
     }
   std::printf("checked %d planned shapes, %d missing\n", checked, bad);
-  return bad ? 1 : 0;
+  // dense_tile_of: every tile of every grid exactly once
+  int orders = 0, bad_orders = 0;
+  static bool seen[64 * 96];
+  for (int tiles_m = 1; tiles_m <= 64; ++tiles_m)
+    for (int tiles_nn = 1; tiles_nn <= 96; ++tiles_nn) {
+      const int tiles = tiles_m * tiles_nn;
+      for (int i = 0; i < tiles; ++i) seen[i] = false;
+      bool ok = true;
+      for (int b = 0; b < tiles && ok; ++b) {
+        const int v = gk::dense_tile_of(b, tiles_m, tiles_nn, 1);
+        const int tn = v >> 16, tm = v & 0xffff;
+        if (tn < 0 || tn >= tiles_nn || tm < 0 || tm >= tiles_m || seen[tn * tiles_m + tm]) ok = false;
+        else seen[tn * tiles_m + tm] = true;
+      }
+      ++orders;
+      if (!ok) {
+        ++bad_orders;
+        std::printf("dense_tile_of: tiles_m=%d tiles_nn=%d is not a bijection\n", tiles_m, tiles_nn);
+      }
+    }
+  std::printf("checked %d tile orders, %d not bijective\n", orders, bad_orders);
+  return (bad || bad_orders) ? 1 : 0;
 }
