@@ -1,8 +1,9 @@
 """Benchmark of the MI355X block-FP8 W8A8 GEMM (BASELINE.json metric).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only qkv|side|prefill|mlp|moe|ceiling]
-    python bench.py --profile config2|prefill|mlp|moe [--reps R]    # eager launches only, for rocprofv3 runs
-    python bench.py --rocprof-summary DIR                          # tables of a rocprofv3 csv output
+    python bench.py --profile config2 [--steps K --warmup W]       # the timed step's graphs, for rocprofv3 runs
+    python bench.py --profile prefill|mlp|moe [--reps R]           # eager launches, for rocprofv3 runs
+    python bench.py --rocprof-summary DIR [--steps K]              # tables of a rocprofv3 csv output
 
 Workload (one "step"): BASELINE.json configs[1] decode sweep -- one block-FP8
 GEMM at each M in {1, 2, 4, 8, 16} with N=6144, K=4096 (QKV projection),
@@ -20,8 +21,8 @@ GEMM B = N*K + 4*ceil(N/128)*ceil(K/128) + 2*M*K + 2*M*N.  Side measurements
 in the same JSON line: the prefill config (M=4096, N=K=7168; TFLOP/s against
 the dense FP8 MFMA peak), the MLP-pair decode config, the MoE layer (512
 tokens, 8 experts, top-2, H=4096, I=14336), the per-M sweep, the
-roofline of the dominant kernel (the decode GEMM with the quantizer fused,
-averaged over the step's five launches; HIP events on its stream), the
+roofline of the dominant kernel (the decode GEMM with the quantizer fused: the
+step's five launches, timed region / 5; HIP events on its stream), the
 prefill kernel's roofline against the dense FP8 MFMA peak (roofline_prefill),
 the streaming-read ceiling of this GPU at the decode footprints
 (stream_ceiling, libgk_probe.so) and the CPU oracle baseline timed on this
@@ -180,12 +181,27 @@ def measured_mfma(kernel_prefix, workload):
     return (busy / cycles, flops, cycles) if seen and cycles > 0 else None
 
 
+def measured_trace(kernel_prefix, workload):
+    """Kernel-trace figures of the timed step from the committed rocprofv3 summaries (`--profile config2` under
+    `--kernel-trace`, summarized by `--rocprof-summary DIR --steps K`): the roofline kernel's average duration over
+    the timed launches and the span of the timed steps per step; None if not recorded."""
+    import re
+    for line in profile_lines():
+        m = re.match(r"trace: kernel=(\S+) workload=(\S+) launches=(\d+) steps=(\d+) avg_us=([0-9.]+) "
+                     r"span_per_step_us=([0-9.]+)", line)
+        if m and m.group(1).startswith(kernel_prefix) and m.group(2) == workload:
+            return {"avg_launch_us": float(m.group(5)), "span_per_step_us": float(m.group(6)),
+                    "launches": int(m.group(3)), "steps": int(m.group(4)),
+                    "source": "profiles/block_fp8_gemm_bench.md (rocprofv3 --kernel-trace of the step graphs)"}
+    return None
+
+
 def kernel_short_name(name):
     """Kernel name without its parameter list (and without the anonymous-namespace marker)."""
     return name.replace("(anonymous namespace)::", "").split("(")[0]
 
 
-def rocprof_summary(directory):
+def rocprof_summary(directory, steps=20):
     """Markdown tables from rocprofv3 csv output: kernel trace durations and PMC counters per dispatch shape.
 
     Dispatches are grouped by (kernel, grid size): one kernel name covers
@@ -213,6 +229,19 @@ def rocprof_summary(directory):
             print(f"| `{name}` | {grid} | {wg} | {len(v)} | {sum(v) / len(v) / 1e3:.2f} | {med(v) / 1e3:.2f} | "
                   f"{min(v) / 1e3:.2f} |")
         print()
+        # The timed step of `--profile config2`: its last len(CONFIG2_MS) x steps dispatches of the roofline kernel
+        # (the warm-up graph's come first): their average duration and the span from the first start to the last
+        # end, per step.
+        rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(open(path))
+                      if kernel_short_name(r["Kernel_Name"]).replace("void ", "").replace(" ", "") ==
+                      DECODE_KERNEL.replace(" ", "") and r["Grid_Size_X"] == "98304")
+        n_timed = len(CONFIG2_MS) * steps
+        if len(rows) >= n_timed:
+            timed = rows[-n_timed:]
+            avg = sum(e - b for b, e in timed) / n_timed / 1e3
+            span = (timed[-1][1] - timed[0][0]) / steps / 1e3
+            print(f"trace: kernel={DECODE_KERNEL.replace(' ', '')} workload=config2_step launches={n_timed} "
+                  f"steps={steps} avg_us={avg:.3f} span_per_step_us={span:.3f}\n")
     counters = defaultdict(list)
     copy = defaultdict(list)  # counter -> values of the calibration copies
     for path in sorted(glob.glob(os.path.join(directory, "**", "*_counter_collection.csv"), recursive=True)):
@@ -292,9 +321,48 @@ def copy_calibration():
     torch.cuda.synchronize()
 
 
-def run_profile(workload, reps):
-    """Eager launches of one workload for rocprofv3 (kernel trace or counters): the same inputs and ops as the
-    timed measurements, no graphs, no timing."""
+CONFIG2_MS = (1, 2, 4, 8, 16)
+CONFIG2_NK = (6144, 4096)
+
+
+class Config2Step:
+    """The timed step (config 2 decode sweep: one block-FP8 GEMM op at each M in CONFIG2_MS, N=6144, K=4096,
+    packed weights rotated over >= 512 MB) and its two HIP graphs: `warm` (W untimed steps) and `timed` (K steps).
+    bench.py times `timed` after replaying `warm`; `--profile config2` replays the same two graphs under rocprofv3,
+    so the profile covers exactly the timed launches."""
+
+    def __init__(self, steps, warmup):
+        from gaudi_kernels import ops
+        from oracle import synth
+        n, k = CONFIG2_NK
+        self.w, self.s = synth.weight(n, k, seed=2000)
+        self.rot = Rotation(self.w, self.s, packed=True)
+        self.xs = {m: synth.activations(m, k, seed=2001 + m).cuda() for m in CONFIG2_MS}
+        self.outs = {m: torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for m in CONFIG2_MS}
+        self.wss = {m: ops.make_workspace(m, n, k) for m in CONFIG2_MS}
+        self.bytes = sum(gemm_bytes(m, n, k) for m in CONFIG2_MS)
+        self.flops = sum(gemm_flops(m, n, k) for m in CONFIG2_MS)
+        self.steps = steps
+
+        def step():
+            for m in CONFIG2_MS:
+                wd, sd = self.rot.next()
+                ops.block_fp8_gemm(self.xs[m], wd, sd, out=self.outs[m], workspace=self.wss[m])
+
+        # The K timed steps (and the W warm-up steps) are captured as HIP graphs so
+        # that the GPU runs them back to back without per-launch host work.
+        self.warm = capture(step, max(1, warmup))
+        self.timed = capture(step, steps)
+
+    def release(self):
+        del self.warm, self.timed
+
+
+def run_profile(workload, reps, steps=20, warmup=5):
+    """One workload's launches for rocprofv3 (kernel trace or counters), no timing.  config2: the timed step's own
+    graphs (`warm` replayed, then `timed` once, as bench.py does; `steps`/`warmup` as its --steps/--warmup), so the
+    last 5 x steps roofline-kernel dispatches of the trace are the timed region.  Others: eager launches of the
+    same inputs and ops as the timed measurements."""
     from gaudi_kernels import ops
     from oracle import synth
 
@@ -302,13 +370,14 @@ def run_profile(workload, reps):
     copy_calibration()
     log(f"[profile] {workload}, {reps} reps")
     if workload == "config2":
-        n, k = 6144, 4096
-        w, s = synth.weight(n, k, seed=2000)
-        p, sd = ops.pack_weight(w.cuda()), s.cuda()
-        for m in (1, 2, 4, 8, 16):
-            x = synth.activations(m, k, seed=2001 + m).cuda()
-            for _ in range(reps):
-                ops.block_fp8_gemm(x, p, sd)
+        c2 = Config2Step(steps, warmup)
+        c2.warm.replay()
+        torch.cuda.synchronize()
+        c2.timed.replay()
+        torch.cuda.synchronize()
+        log(f"[profile] config2 step graph: {warmup} warm-up steps, then {steps} timed steps of "
+            f"{len(CONFIG2_MS)} launches")
+        c2.release()
     elif workload == "prefill":
         m, n, k = 4096, 7168, 7168
         w, s = synth.weight(n, k, seed=4000)
@@ -463,8 +532,8 @@ def cpu_baselines(w2, s2):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--only", choices=["decode", "qkv", "side", "prefill", "mlp", "moe", "ceiling"], default=None)
     ap.add_argument("--rocprof-summary", metavar="DIR", default=None,
@@ -474,7 +543,7 @@ def main():
     ap.add_argument("--reps", type=int, default=5)
     args = ap.parse_args()
     if args.rocprof_summary:
-        rocprof_summary(args.rocprof_summary)
+        rocprof_summary(args.rocprof_summary, args.steps)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (under tensor parallelism each GPU "
@@ -482,7 +551,7 @@ def main():
         sys.exit(2)
 
     if args.profile:
-        run_profile(args.profile, args.reps)
+        run_profile(args.profile, args.reps, args.steps, args.warmup)
         return
 
     from gaudi_kernels import ops
@@ -494,37 +563,23 @@ def main():
     result = {}
 
     # ---- config 2: decode sweep (the timed step) ----------------------------------------------
-    n, k = 6144, 4096
-    ms_list = (1, 2, 4, 8, 16)
-    w, s = synth.weight(n, k, seed=2000)
-    rot = Rotation(w, s, packed=True)
+    n, k = CONFIG2_NK
+    ms_list = CONFIG2_MS
+    c2 = Config2Step(args.steps, args.warmup)
+    w, s, rot, xs, outs, wss = c2.w, c2.s, c2.rot, c2.xs, c2.outs, c2.wss
     rot_row = Rotation(w, s)
-    xs = {m: synth.activations(m, k, seed=2001 + m).cuda() for m in ms_list}
-    outs = {m: torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for m in ms_list}
-    wss = {m: ops.make_workspace(m, n, k) for m in ms_list}
-    sweep_bytes = sum(gemm_bytes(m, n, k) for m in ms_list)
-    sweep_flops = sum(gemm_flops(m, n, k) for m in ms_list)
-
-    def step():
-        for m in ms_list:
-            wd, sd = rot.next()
-            ops.block_fp8_gemm(xs[m], wd, sd, out=outs[m], workspace=wss[m])
-
-    # The K timed steps (and the W warm-up steps) are captured as HIP graphs so
-    # that the GPU runs them back to back without per-launch host work.
+    sweep_bytes, sweep_flops = c2.bytes, c2.flops
     log(f"[bench] decode sweep: {len(rot.items)} weight copies, warmup {args.warmup}, steps {args.steps}")
-    g_warm = capture(step, max(1, args.warmup))
-    g_timed = capture(step, args.steps)
-    g_warm.replay()
+    c2.warm.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
-    g_timed.replay()
+    c2.timed.replay()
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    del g_warm, g_timed
+    c2.release()
     ms_per_step = ev0.elapsed_time(ev1) / args.steps
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"[bench] decode sweep {ms_per_step * 1e3:.1f} us/step, {value:.0f} GB/s (wall {wall:.3f}s)")
@@ -554,23 +609,29 @@ def main():
         log(f"[bench]   M={m}: op {op_ms * 1e3:.2f} us ({per_m[str(m)]['op_GBps']} GB/s), "
             f"kernel on pre-quantized activations {kern_ms * 1e3:.2f} us "
             f"({per_m[str(m)]['q_path_kernel_GBps']} GB/s), row-major weights {row_ms * 1e3:.2f} us")
-    del rot, rot_row
+    del rot, rot_row, c2
     torch.cuda.empty_cache()
 
     copy_calibration()
 
-    # Average launch of the step's kernel: algorithmic bytes per launch (the
-    # mean over M = 1..16 of N*K + 4*(N/128)*(K/128) + 2*M*K + 2*M*N) over the
-    # mean launch duration.
+    # The roofline kernel's average launch over the timed region: the step is the kernel's five launches (one per
+    # M) and nothing else, so a launch takes ms_per_step / 5 (HIP events on the replay stream, the launch gaps of
+    # the graph included).  Algorithmic bytes per launch: the mean over M = 1..16 of
+    # N*K + 4*(N/128)*(K/128) + 2*M*K + 2*M*N.  The committed kernel trace of the same graphs
+    # (`--profile config2`) gives the kernel-only duration and the span of the timed steps beside it.
     avg_bytes = sweep_bytes / len(ms_list)
-    avg_us = sum(launch_us) / len(launch_us)
+    avg_us = ms_per_step * 1e3 / len(ms_list)
     achieved = avg_bytes / (avg_us * 1e-6) / 1e9
+    trace = measured_trace(DECODE_KERNEL, "config2_step")
     result["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(achieved / PEAK_HBM_GBS, 4),
                           "traffic": measured_traffic(DECODE_KERNEL, "config2"),
-                          "traffic_source": "profiles/ (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
+                          "traffic_source": "profiles/ (rocprofv3 FETCH_SIZE/WRITE_SIZE of the timed step graphs)",
                           "kernel": f"{DECODE_KERNEL} (quantizer fused; M=1,2,4,8,16, N=6144, K=4096, packed weights)",
                           "bytes_per_launch": int(avg_bytes), "avg_launch_us": round(avg_us, 3),
+                          "launch_us_source": "timed region: ms_per_step / 5 launches (HIP events, gaps included)",
+                          "profile": trace,
+                          "steady_state_launch_us": {str(m): round(t, 3) for m, t in zip(ms_list, launch_us)},
                           "m16": {"achieved": round(gemm_bytes(16, n, k) / (launch_us[-1] * 1e-6) / 1e9, 1),
                                   "launch_us": round(launch_us[-1], 3)}}
     result["decode_sweep"] = per_m
