@@ -25,7 +25,7 @@ roofline of the dominant kernel (the decode GEMM with the quantizer fused: the
 step's five launches, timed region / 5; HIP events on its stream), the
 prefill kernel's roofline against the dense FP8 MFMA peak (roofline_prefill),
 the streaming-read ceiling of this GPU at the decode footprints
-(stream_ceiling, libgk_probe.so) and the CPU oracle baseline timed on this
+(stream_ceiling, tests/csrc/libgk_probe.so) and the CPU oracle baseline timed on this
 host (config 2 M=16 as cpu_baseline; configs 3, 4 and 5 beside it).
 """
 
@@ -418,11 +418,11 @@ def moe_inputs(device="cuda"):
 
 
 def stream_ceiling():
-    """Best streaming-read rate (GB/s) of a plain read kernel (libgk_probe.so) at the decode footprints: config 2's
+    """Best streaming-read rate (GB/s) of a plain read kernel (tests/csrc/libgk_probe.so) at the decode footprints: config 2's
     weights (25.17 MB) and config 3's gate_up weights (117.44 MB), buffers rotated over >= 512 MB like the GEMMs,
     workgroup counts 256..4096."""
     import ctypes
-    path = os.path.join(ROOT, "gaudi-kernels_amd", "python", "gaudi_kernels", "libgk_probe.so")
+    path = os.path.join(ROOT, "tests", "csrc", "libgk_probe.so")
     lib = ctypes.CDLL(path)
     lib.gk_probe_stream_read.restype = ctypes.c_int
     lib.gk_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,

@@ -77,28 +77,6 @@ def compile_one(src, debug):
     return obj, warn
 
 
-PROBE_SRC = CSRC / "gk_probe.hip"
-PROBE_LIB = OUT_DIR / "libgk_probe.so"
-
-
-def build_probe(verbose=True):
-    """libgk_probe.so: the streaming-read probe bench.py measures the HBM ceiling with, and the exhaustive check
-    of the kernels' hardware bf16 rounding and E4M3 encode (not the GEMM library)."""
-    OBJ_DIR.mkdir(exist_ok=True)
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-shared", "-Wl,-z,defs", str(PROBE_SRC), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{res.stderr}")
-    os.replace(tmp, PROBE_LIB)
-    have = exported_symbols(PROBE_LIB)
-    if have != ["gk_probe_bf16x2_check", "gk_probe_e4m3_check", "gk_probe_stream_read"]:
-        raise RuntimeError(f"probe exports {have}")
-    if verbose:
-        print(f"built {PROBE_LIB}")
-    return PROBE_LIB
-
-
 def build(jobs=4, debug=False, verbose=True):
     OBJ_DIR.mkdir(exist_ok=True)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
@@ -117,7 +95,6 @@ def build(jobs=4, debug=False, verbose=True):
     syms = verify_abi(LIB)
     if verbose:
         print(f"built {LIB} ({LIB.stat().st_size} bytes), {len(syms)} exported entry points")
-    build_probe(verbose)
     return LIB
 
 

@@ -38,8 +38,10 @@ constexpr const char* kOps[] = {
     "gk_gelu_and_mul_bf16_v1",      // gelu_and_mul_bf16.c, glue generic_dense_glue.cpp:424-458
     "gk_fp8_gelu_mul_quant_bf16_v1",  // GELU-and-mul fused with the 1x128 quantizer (build-defined)
     "gk_fp8_moe_route_v1",          // MoE routing + expert-sorted layout (build-defined)
-    "gk_fp8_moe_bf16_v1",           // block-FP8 MoE layer (build-defined)
+    "gk_fp8_moe_bf16_v2",           // block-FP8 MoE layer (build-defined); v2: packed
+                                    // experts are gk_fp8_pack_experts' panel-major layout
     "gk_fp8_pack_weight_v1",        // load-time layout packing (fp8_codec.py:19 "a separate step")
+    "gk_fp8_pack_experts_v1",       // the same for the MoE layer's expert weights, panel-major
     "gk_rms_norm_bf16_v1",          // rms_norm_bf16.c, glue generic_dense_glue.cpp:135-190
     "gk_fused_add_rms_norm_bf16_v1",  // fused_add_rms_norm_bf16.c, same glue
     "gk_fp8_rms_norm_quant_bf16_v1",  // (fused add +) RMSNorm fused with the 1x128 quantizer (build-defined)

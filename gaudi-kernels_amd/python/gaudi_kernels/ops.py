@@ -693,6 +693,9 @@ def partial_finish(partial, bias=None, *, out=None):
         raise ValueError("expected a contiguous fp32 bias with `width` elements on the same GPU")
     if out is None:
         out = torch.empty((rows, width), dtype=torch.bfloat16, device=device)
+    elif (out.dtype != torch.bfloat16 or out.ndim != 2 or tuple(out.shape) != (rows, width) or out.stride(1) != 1
+          or out.device != device):
+        raise ValueError("out must be a bf16 [rows, width] tensor with unit column stride on the partial's GPU")
     lib = nat.load()
     nat.check("gk_fp8_partial_finish_bf16",
               lib.gk_fp8_partial_finish_bf16(_ptr(partial), rows, width, partial.stride(0), _ptr(bias), _ptr(out),

@@ -60,7 +60,8 @@ typedef enum gk_status {
 #define GK_FLAG_FORCE_PREFILL 4u   /* force the LDS-tiled MFMA variant */
 #define GK_FLAG_FORCE_GENERIC 8u   /* force the any-shape variant */
 #define GK_FLAG_DECODE_LAYOUT 16u  /* act_quant / q GEMM only: quantized activations in the decode fragment layout */
-#define GK_FLAG_WEIGHT_PACKED 32u  /* block GEMMs, MoE layer: weights packed by gk_fp8_pack_weight (not the generic variant) */
+#define GK_FLAG_WEIGHT_PACKED 32u  /* block GEMMs: weights packed by gk_fp8_pack_weight (not the generic variant);
+                                      MoE layer: experts packed by gk_fp8_pack_experts (op gk_fp8_moe_bf16_v2) */
 #define GK_FLAG_ACCUMULATE 64u     /* K-slice GEMM only: add into the fp32 partial instead of overwriting it */
 
 /* Variants reported by gk_fp8_block_gemm_plan. */
@@ -179,7 +180,10 @@ gk_status gk_fp8_block_gemm_bf16(const void* x, int64_t m, int64_t k, int64_t ld
                                  void* stream);
 
 /* Scratch of gk_fp8_block_gemm_bf16_noalloc (bytes, per GPU): enough for
- * the quantized activations of config 4's M = 4096, K = 7168. */
+ * the quantized activations of config 4's M = 4096, K = 7168.  The array is
+ * part of the library's code object, so loading the library reserves these
+ * 32 MiB of device memory on every GPU the process runs the library's
+ * kernels on, whether or not this entry point is ever called. */
 #define GK_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* gk_fp8_block_gemm_bf16 without a workspace argument and without any

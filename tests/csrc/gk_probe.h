@@ -1,4 +1,5 @@
-/* gk_probe.h -- measurement probe used by bench.py (libgk_probe.so).  Not part
+/* gk_probe.h -- measurement probe used by bench.py and the tests
+ * (tests/csrc/libgk_probe.so, built by tests/csrc/build_probe.py).  Not part
  * of the block-FP8 library and not a reference interface: it has no
  * counterpart in the reference, which publishes no performance figures.
  *

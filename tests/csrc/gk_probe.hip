@@ -1,4 +1,5 @@
-// Measurement probe for bench.py (libgk_probe.so, declared in include/gk_probe.h):
+// Measurement probe for bench.py and the tests (tests/csrc/libgk_probe.so, declared in gk_probe.h beside
+// this file, built by tests/csrc/build_probe.py):
 // a plain streaming read of device memory, the ceiling any weight-streaming
 // kernel can reach on this GPU for a given footprint.  Not part of the GEMM
 // library.  Each lane reads 16-byte pieces with non-temporal loads (as the
@@ -16,7 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/gk_probe.h"
+#include "gk_probe.h"
 #include "gk_fp8_internal.h"
 
 namespace {

@@ -44,6 +44,9 @@ def test_load_version_and_ops():
     names = nat.list_ops()
     assert "gk_fp8_block_gemm_bf16_v1" in names and "gk_fp8_codec_ocp_to_half_v1" in names
     assert len(names) == len(set(names))
+    # the MoE layer's packed-expert layout changed: the op is v2, beside its packing op
+    assert "gk_fp8_moe_bf16_v2" in names and "gk_fp8_moe_bf16_v1" not in names
+    assert "gk_fp8_pack_experts_v1" in names
     # capacity smaller than the table -> names filled up to capacity + INSUFFICIENT_BUFFER
     cap = ctypes.c_uint32(2)
     arr = (ctypes.c_char_p * 2)()
@@ -271,12 +274,12 @@ def test_partial_finish_rejections_before_device_use():
 
 
 def test_probe_library_exports_match_its_header():
-    """libgk_probe.so (bench.py's streaming-read ceiling, the hardware conversion checks) exports exactly what
-    include/gk_probe.h declares."""
-    probe = os.path.join(os.path.dirname(nat.lib_path()), "libgk_probe.so")
+    """tests/csrc/libgk_probe.so (bench.py's streaming-read ceiling, the hardware conversion checks; not part of
+    the library) exports exactly what tests/csrc/gk_probe.h declares."""
+    probe = os.path.join(ROOT, "tests", "csrc", "libgk_probe.so")
     if not os.path.exists(probe):
         pytest.skip("libgk_probe.so not built")
-    text = open(os.path.join(ROOT, "include", "gk_probe.h")).read()
+    text = open(os.path.join(ROOT, "tests", "csrc", "gk_probe.h")).read()
     want = sorted(set(re.findall(r"^\s*int\s+(gk_\w+)\s*\(", text, re.MULTILINE)))
     out = subprocess.run(["nm", "-D", "--defined-only", probe], check=True, capture_output=True, text=True).stdout
     have = sorted({l.split()[-1] for l in out.splitlines() if " T " in l and l.split()[-1].startswith("gk_")})
@@ -293,3 +296,15 @@ def test_probe_library_exports_match_its_header():
     lib.gk_probe_e4m3_check.restype = ctypes.c_int
     lib.gk_probe_e4m3_check.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     assert lib.gk_probe_e4m3_check(None, None) == 1
+
+
+def test_noalloc_rejects_beyond_scratch():
+    """gk_fp8_block_gemm_bf16_noalloc checks its plan against GK_NOALLOC_SCRATCH_BYTES before any device work:
+    a plan needing more scratch returns GK_INSUFFICIENT_BUFFER (fake pointers are never touched; host-only test)."""
+    lib = nat.load()
+    m, n, k = 8192, 7168, 7168          # 8192 x 56 groups x 132 B > 32 MiB of scratch
+    _, _, need = ops.plan(m, n, k)
+    assert need > (32 << 20)
+    fake = ctypes.c_void_p(1 << 20)
+    st = lib.gk_fp8_block_gemm_bf16_noalloc(fake, m, k, k, fake, n, fake, 56, 56, None, fake, n, 0, None)
+    assert st == nat.GK_INSUFFICIENT_BUFFER

@@ -138,6 +138,20 @@ def test_config4_prefill_sampled_rows_and_invariants():
     assert torch.equal(y2.view(torch.int16), (y.float() * 2).bfloat16().view(torch.int16))
 
 
+@pytest.mark.timeout(600)
+def test_config4_prefill_all_rows_packed_op():
+    """Config 4 in the form bench.py times it: weights packed at load time, the op's 1x128 quantizer, then the
+    one-launch split GEMM (256-wide tiles on 4096 columns, 192-wide on 3072) -- every one of the 4096 rows
+    against the oracle (64-row chunks of the fp64 restatement: about 5 s on 16 host cores)."""
+    m, n, k = 4096, 7168, 7168
+    w, s = synth.weight(n, k, seed=4000)
+    x = synth.activations(m, k, seed=4001)
+    assert ops.plan(m, n, k)[0] == ops.nat.GK_VARIANT_PREFILL
+    y = ops.block_fp8_gemm(x.cuda(), ops.pack_weight(w.cuda()), s.cuda()).cpu()
+    ref = block_fp8.reference(x, w, s, row_chunk=64)
+    assert_parity(y, ref, "config 4, all rows, packed weights")
+
+
 @pytest.mark.parametrize("m,n,k", [(16, 200, 256), (17, 130, 512), (129, 384, 1024), (300, 1000, 768),
                                    (3, 2048, 2048), (64, 128, 128), (33, 1000, 768), (48, 2048, 1024)])
 @pytest.mark.parametrize("native_half", [False, True])

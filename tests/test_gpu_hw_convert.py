@@ -16,13 +16,13 @@ import os
 import pytest
 import torch
 
-from gaudi_kernels import _native as nat
-
 pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def run_check(name):
-    lib = ctypes.CDLL(os.path.join(os.path.dirname(nat.lib_path()), "libgk_probe.so"))
+    lib = ctypes.CDLL(os.path.join(ROOT, "tests", "csrc", "libgk_probe.so"))
     fn = getattr(lib, name)
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]

@@ -26,9 +26,12 @@ pytestmark = pytest.mark.gpu
 # the device's own input, max 6e-3 / mean 5e-5 measured).  End to end, a one-ulp
 # bf16 difference in the gate_up output flips ~6% of the affected E4M3 codes of
 # the requantized intermediate (relative step 6-12%), and those flips sum over
-# K = 14336 in the down GEMM: measured max 2.2e-2 / mean 2.1e-3 on this input.
-CHAIN_MAX_REL = 4e-2
-CHAIN_MEAN_REL = 4e-3
+# K = 14336 in the down GEMM: measured max 1.628e-2 / mean 1.628e-3 on this
+# input (the kernels are deterministic, so this is the one value), inside the
+# GEMM gate's mean bound and 1.6x its max bound.  The bound sits just above it,
+# so a regression shows.
+CHAIN_MAX_REL = 2e-2
+CHAIN_MEAN_REL = 2e-3
 
 
 def check_routing(logits, top_k):

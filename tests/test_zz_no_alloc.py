@@ -65,11 +65,40 @@ def test_noalloc_matches_workspace_entry_twice(seq, native_half):
         assert torch.equal(y_ref.view(torch.int16), y_na.view(torch.int16)), (m, n, k, i)
 
 
-def test_noalloc_rejects_beyond_scratch():
+@pytest.mark.parametrize("m,n,k", [(16, 28672, 4096), (8, 6144, 4096), (1024, 2048, 7168)],
+                         ids=["decode-scratch", "decode-fused", "prefill"])
+def test_noalloc_under_graph_capture(m, n, k):
+    """The entry's stated use: a caller that captures it in a HIP graph.  After one eager call (the per-device
+    set-up: the scratch's symbol address, the LDS limit of the tiled kernels), the call is captured; each of three
+    replays -- with eager work between them, including an eager call of another shape that rewrites the shared
+    scratch -- gives the eager result bit for bit."""
     lib = nat.load()
-    m, n, k = 8192, 7168, 7168          # 8192 x 56 groups x 132 B > 32 MiB of scratch
-    _, _, need = ops.plan(m, n, k)
-    assert need > (32 << 20)
-    fake = ctypes.c_void_p(1 << 20)
-    st = lib.gk_fp8_block_gemm_bf16_noalloc(fake, m, k, k, fake, n, fake, 56, 56, None, fake, n, 0, None)
-    assert st == nat.GK_INSUFFICIENT_BUFFER
+    w, s = synth.weight(n, k, seed=n + k, device="cuda")
+    x = synth.activations(m, k, seed=m).cuda()
+    w8 = w.view(torch.uint8)
+    x_other, (w_other, s_other) = synth.activations(40, 1024, seed=5).cuda(), synth.weight(512, 1024, seed=6, device="cuda")
+    y_other = torch.empty((40, 512), dtype=torch.bfloat16, device="cuda")
+
+    def call(xx, ww, ss, y):
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        mm, kk = xx.shape
+        nn = ww.shape[0]
+        nat.check("gk_fp8_block_gemm_bf16_noalloc",
+                  lib.gk_fp8_block_gemm_bf16_noalloc(_p(xx), mm, kk, xx.stride(0), _p(ww.view(torch.uint8)), nn, _p(ss),
+                                                     ss.shape[0], ss.shape[1], None, _p(y), nn, 0, stream))
+
+    y_eager = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    call(x, w8, s, y_eager)
+    torch.cuda.synchronize()
+    y_graph = torch.full((m, n), 3.0, dtype=torch.bfloat16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call(x, w8, s, y_graph)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y_graph.fill_(3.0)
+        call(x_other, w_other, s_other, y_other)  # rewrites the scratch between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph.view(torch.int16), y_eager.view(torch.int16))
