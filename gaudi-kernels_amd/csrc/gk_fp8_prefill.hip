@@ -402,6 +402,13 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
       // step's reads end with lgkmcnt(0)).  A bare barrier: __syncthreads()'s
       // release fence would wait for the weight loads still in flight.
       __builtin_amdgcn_s_barrier();
+      // Dense: the two waves of a SIMD (wm = 0, 1) share its matrix core, and
+      // the issue arbiter favours the older one, which then waits at the next
+      // barrier while the younger one finishes alone (measured on MI355X with
+      // per-step timers, config 4: about 900 of 3000 cycles a step).  The
+      // younger wave runs the first half of the step (blocks 0..3) at raised
+      // priority; both are back at 0 from block 4 (config 4 GEMM: -2%).
+      if (!GROUPED && wm) __builtin_amdgcn_s_setprio(1);
       const int as_next = as ^ 1, ws_free = ws == 0 ? 2 : ws - 1;  // the stages step g-1 used
       // Dense GEMMs (MFMA-bound) spread the step's loads between the token
       // blocks; the grouped form (bound by the weight stream) issues them all
@@ -446,6 +453,9 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
         // blocks past the live rows are skipped (a wave-uniform branch).  Dense
         // GEMMs have at most one partial row tile and keep the branch-free step.
         const bool skip = GROUPED && j >= jl;
+        if constexpr (j == 4) {
+          if (!GROUPED) __builtin_amdgcn_s_setprio(0);
+        }
         if (kSpread) {  // this step's tile loads, spread over the first blocks
           if (j < 4) {
             issue_a_one(min(g + 1, gend - 1), as_next, j);
@@ -592,6 +602,52 @@ __device__ __forceinline__ void prefill256_body(int block, const uint8_t* __rest
               if (n + r < N) dst[r] = v[r];
           }
         }
+      }
+    }
+    return;
+  }
+  if (!GROUPED && (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (ldy & 7) == 0) {
+    // Dense bf16 tile through LDS (free once every wave is past its last
+    // fragment read and its own copies have landed): rows of BN * 2 bytes at
+    // a stride of BN * 2 + 16, then whole-row 16-byte stores.  The fragment
+    // layout would store 32-byte pieces of 16 rows per instruction; every
+    // workgroup of a round stores its tile at once, so the epilogue is a
+    // write burst (measured on MI355X, config 4 GEMM: -1%).  Same bits as
+    // store_tile: bias added in fp32, one bf16 rounding.
+    constexpr int kRS = BN * 2 + 16, kCPR = BN / 8;  // LDS row stride; 16-byte chunks per row
+    static_assert(kBM * kRS <= kLdsBytes, "the staged tile fits the LDS");
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int nl = wn * 16 * NA + i * 16 + 4 * fq, ml = mw + j * kJS + fr;
+        float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) b[r] = (n0 + nl + r < N) ? bias[n0 + nl + r] : 0.0f;
+        }
+        const uint32_t h01 = bf16x2_rne(acc[i][j][0] + b[0], acc[i][j][1] + b[1]);
+        const uint32_t h23 = bf16x2_rne(acc[i][j][2] + b[2], acc[i][j][3] + b[3]);
+        *reinterpret_cast<uint2*>(smem + ml * kRS + nl * 2) = make_uint2(h01, h23);
+      }
+    }
+    __syncthreads();
+    const int rows = min(live, kBM);
+#pragma unroll 4
+    for (int it = tid; it < kBM * kCPR; it += 512) {
+      const int r = it / kCPR, c = it - r * kCPR;
+      if (r >= rows) break;
+      const uint4 v = *reinterpret_cast<const uint4*>(smem + r * kRS + c * 16);
+      const int n = n0 + c * 8;
+      uint16_t* dst = y + static_cast<int64_t>(m0 + r) * ldy + n;
+      if (n + 7 < N) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        const uint32_t h[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) dst[e] = static_cast<uint16_t>(h[e >> 1] >> (16 * (e & 1)));
       }
     }
     return;
