@@ -35,6 +35,9 @@
 //     straight-line code, which the scheduler interleaves freely.
 //   * 16x16 output layout: lane l, register r -> n = 4 (l/16) + r, m = l % 16:
 //     one token per lane, so the promotion factor is one scalar per block.
+//   * Dense tiles: the younger wave of each SIMD runs the first half of a step
+//     at raised priority (the two share the matrix core), and the bf16 tile
+//     leaves through LDS as whole-row 16-byte stores.
 
 #include <mutex>
 #include <type_traits>
