@@ -186,6 +186,33 @@ def test_output_padding_untouched():
         assert bool((raw[:mm, n:] == SENTINEL).all()) and bool((raw[mm:] == SENTINEL).all())
 
 
+@pytest.mark.parametrize("m,n", [(300, 203), (256, 200), (40, 1000)])
+def test_prefill_epilogue_forms_same_bits(m, n):
+    """The prefill tile leaves through LDS as whole-row 16-byte stores when y is 16-byte aligned with a row stride
+    that is a multiple of 8, and through per-fragment stores otherwise: both forms write the same bits, only
+    inside [M, N] (a ragged last 16-byte chunk included), and match the oracle."""
+    k = 512
+    w, s = synth.weight(n, k, seed=n + 3)
+    x = synth.activations(m, k, seed=m + 4)
+    b = torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1
+    ref = block_fp8.reference(x, w, s, bias=b)
+    results = []
+    for ld, off in ((n + (-n) % 8 + 8, 0), (n + 3, 0), (n + (-n) % 8 + 8, 1)):  # staged, odd stride, misaligned y
+        buf = torch.full((m + 2, ld + 8), SENTINEL, dtype=torch.int16, device="cuda").view(torch.bfloat16)
+        flat = buf.view(-1)[off: off + m * ld].view(m, ld)
+        out = flat[:, :n]
+        ops.block_fp8_gemm(x.cuda(), w.cuda(), s.cuda(), b.cuda(), variant="prefill", out=out)
+        torch.cuda.synchronize()
+        raw = buf.view(torch.int16).view(-1)
+        written = torch.zeros_like(raw, dtype=torch.bool)
+        idx = (off + torch.arange(m, device="cuda")[:, None] * ld + torch.arange(n, device="cuda")[None, :]).view(-1)
+        written[idx] = True
+        assert bool((raw[~written] == SENTINEL).all()), f"ld={ld} off={off}: a write outside [M, N]"
+        results.append(out.cpu().view(torch.int16).clone())
+        assert_parity(out.cpu(), ref, f"{m}x{n} ld={ld} off={off}")
+    assert torch.equal(results[0], results[1]) and torch.equal(results[0], results[2])
+
+
 def test_drop_in_reference_api_cpu_tensors():
     case = CASES[0]
     y = gpu_oracle.reference(case["x"], case["w"], case["scales"])
