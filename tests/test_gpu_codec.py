@@ -72,7 +72,7 @@ def test_shape_dtype_and_contiguity():
         reencode_e4m3fn_half(weight, scales.to(torch.float64))
 
 
-@pytest.mark.parametrize("n", [1, 15, 16, 17, 4095, 1 << 20, (1 << 24) + 3])
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 4095, 1 << 20, (1 << 24) + 3, (1 << 24) + 16 * 5 + 3])
 def test_device_sweep_bit_exact(n):
     gen = torch.Generator().manual_seed(n)
     codes = torch.randint(0, 256, (n,), generator=gen, dtype=torch.uint8)
