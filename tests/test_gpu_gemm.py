@@ -77,6 +77,32 @@ def test_config2_packed_fused_quantizer_against_oracle(m):
     assert_parity(y, block_fp8.reference(x, w, s), f"packed fused M={m}")
 
 
+@pytest.mark.parametrize("m", [1, 16])
+def test_config2_native_half_packed_fused_against_oracle(m):
+    """The benchmarked decode form in native_half mode: Gaudi2 half-range codes from the GPU codec, packed, the
+    quantizer fused (half-range activation codes, doubled scales), against the oracle's native_half path."""
+    n, k = 6144, 4096
+    w, s = synth.weight(n, k, seed=2000)
+    x = synth.activations(m, k, seed=2101 + m)
+    wh, sh, _ = ops.codec_ocp_to_half(w.cuda(), s.cuda())
+    y = ops.block_fp8_gemm(x.cuda(), ops.pack_weight(wh), sh, native_half=True).cpu()
+    ref = block_fp8.reference(x, wh.cpu().view(torch.float8_e4m3fn), sh.cpu(), native_half=True)
+    assert_parity(y, ref, f"native_half packed fused M={m}")
+
+
+def test_config4_native_half_split_sampled_rows():
+    """Config 4 through the split prefill launch in native_half mode (half-range weight codes widened in the
+    kernel, doubled scales) on packed weights, against the oracle on 48 sampled rows."""
+    m, n, k = 4096, 7168, 7168
+    w, s = synth.weight(n, k, seed=4000)
+    x = synth.activations(m, k, seed=4101)
+    wh, sh, _ = ops.codec_ocp_to_half(w.cuda(), s.cuda())
+    y = ops.block_fp8_gemm(x.cuda(), ops.pack_weight(wh), sh, native_half=True)
+    rows = torch.randperm(m, generator=torch.Generator().manual_seed(3))[:48].sort().values
+    ref = block_fp8.reference(x[rows], wh.cpu().view(torch.float8_e4m3fn), sh.cpu(), native_half=True, row_chunk=16)
+    assert_parity(y[rows.cuda()].cpu(), ref, "native_half prefill sampled rows")
+
+
 def test_config3_packed_against_oracle():
     m = 16
     for (n, k, seed) in ((28672, 4096, 3000), (4096, 14336, 3100)):
